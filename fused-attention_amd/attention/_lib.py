@@ -1,0 +1,132 @@
+"""ctypes binding of libfa.so, the gfx950 HIP library behind every fused backend.
+
+The library exports the C ABI declared in include/fa.h.  It is built in-tree
+(``make -C fused-attention_amd/csrc``) and loaded from the package root.  There
+is no fallback: if the library is missing, every fused entry point raises.
+"""
+
+import ctypes
+import math
+import os
+
+import torch
+
+LOG2E = 1.4426950408889634  # log2(e), folded with 1/sqrt(D) as in attention/fused/fused.py:74
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.environ.get("FA_LIB_PATH", os.path.join(_PKG_ROOT, "libfa.so"))
+
+FA_F16, FA_BF16 = 0, 1
+_DTYPE_CODE = {torch.float16: FA_F16, torch.bfloat16: FA_BF16}
+
+FA_OK = 0
+FA_ERR_DIMS = -1
+FA_ERR_DTYPE = -2
+FA_ERR_HEADDIM = -3
+FA_ERR_TILE = -4
+FA_ERR_NULL = -5
+FA_ERR_LAUNCH = -6
+FA_ERR_UNSUPPORTED = -7
+
+# (name, restype, argtypes) for every symbol of include/fa.h
+_VP, _I, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "fa_fwd": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _F, _I, _I, _VP]),
+    "fa_bwd": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                    _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
+    "fa_supported": (_I, [_I, _I, _I, _I, _I, _I, _I]),
+    "fa_strerror": (ctypes.c_char_p, [_I]),
+    "fa_version": (_I, []),
+}
+
+_lib = None
+
+
+class LibraryError(RuntimeError):
+    """libfa.so is missing or could not be loaded."""
+
+
+def load():
+    """Load libfa.so once; raise LibraryError (never fall back) if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryError(
+            f"{LIB_PATH} not found; build it with `make -C fused-attention_amd/csrc` "
+            f"(or __graft_entry__.build()) before using the fused backends")
+    try:
+        lib = ctypes.CDLL(LIB_PATH)
+    except OSError as e:
+        raise LibraryError(f"could not load {LIB_PATH}: {e}") from e
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def strerror(code):
+    return load().fa_strerror(code).decode()
+
+
+def dtype_code(dtype):
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"fused kernels support float16 and bfloat16, got {dtype}") from None
+
+
+def scale_log2(D):
+    return LOG2E / math.sqrt(D)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("fused kernels need GPU tensors; move Q, K, V to the GPU first")
+
+
+def check(code, what):
+    """Map a negative status to the reference's exception types."""
+    if code == FA_OK:
+        return
+    msg = f"{what}: {strerror(code)} (status {code})"
+    if code == FA_ERR_DTYPE:
+        raise TypeError(msg)
+    if code in (FA_ERR_DIMS, FA_ERR_HEADDIM, FA_ERR_TILE, FA_ERR_NULL, FA_ERR_UNSUPPORTED):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def fwd(q, k, v, o, lse, tile_m, tile_n):
+    """Enqueue the forward on the current stream.  Shapes already checked by the caller."""
+    lib = load()
+    _require_device(q, k, v, o)
+    B, H, S, D = q.shape
+    H_kv = k.shape[1]
+    code = lib.fa_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
+                      B, H, H_kv, S, D, dtype_code(q.dtype), scale_log2(D),
+                      int(tile_m), int(tile_n), _stream(q.device))
+    check(code, "fa_fwd")
+
+
+def bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n):
+    """Enqueue dK/dV then dQ on the current stream."""
+    lib = load()
+    _require_device(q, k, v, o, do, lse, dq, dk, dv)
+    B, H, S, D = q.shape
+    code = lib.fa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
+                      _ptr(dq), _ptr(dk), _ptr(dv), B, H, S, D, dtype_code(q.dtype),
+                      scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
+                      _stream(q.device))
+    check(code, "fa_bwd")

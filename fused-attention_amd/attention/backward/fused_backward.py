@@ -1,0 +1,73 @@
+"""Fused causal attention with a recompute backward and autograd, on MI355X.
+
+Drop-in for attention/backward/fused_backward.py:151-206 of the reference.
+
+Forward  = the fused forward kernel with the LSE output switched on: it writes
+           lse = m + log2(l) (base-2 log-sum-exp of the scores pre-multiplied by
+           log2(e)/sqrt(D)) directly, where the reference stores m and l and adds
+           them with a torch op (:61-62, :169).
+Backward = two atomic-free kernels on the same stream:
+  dK/dV kernel: one workgroup per key tile; loops over the query tiles that see it,
+                recomputing P from the LSE; dV = P^T dO, dK = scale * dS^T Q.
+  dQ kernel:    one workgroup per query tile; loops over the visible key tiles;
+                dQ = scale * dS K.
+  with dS = P * (dP - Delta), dP = dO V^T and Delta = rowsum(dO * O) computed
+  inside both kernels from the O and dO rows they already read (the reference
+  runs it as a separate torch op, :175).
+
+Shapes: q, k, v are (B, H, N, D) float16 or bfloat16, N divisible by both tiles.
+Use:    o = fused_attention_autograd(q, k, v, tile_m=64, tile_n=64); o.backward(do)
+"""
+
+import torch
+
+from attention import _lib
+
+_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def _check(q, k, v, tile_m, tile_n):
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q, k, v must all be float16 or all be bfloat16")
+    if q.shape != k.shape or q.shape != v.shape or q.dim() != 4:
+        raise ValueError(f"q, k, v must all be (B, H, N, D); got {q.shape}, {k.shape}, {v.shape}")
+    N = q.shape[2]
+    if N % tile_m or N % tile_n:
+        raise ValueError(f"N={N} must be divisible by tile_m={tile_m} and tile_n={tile_n}")
+
+
+def _forward(q, k, v, tile_m, tile_n):
+    """Returns (o, lse) with lse [B, H, N] float32 in the reference's base-2 units."""
+    B, H, N, D = q.shape
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    _lib.fwd(q, k, v, o, lse, tile_m, tile_n)
+    return o, lse
+
+
+def _backward(q, k, v, o, lse, do, tile_m, tile_n):
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    _lib.bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n)
+    return dq, dk, dv
+
+
+class FusedAttentionFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, tile_m=64, tile_n=64):
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        _check(q, k, v, tile_m, tile_n)
+        o, lse = _forward(q, k, v, tile_m, tile_n)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.tiles = (tile_m, tile_n)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = _backward(q, k, v, o, lse, do.contiguous().to(q.dtype), *ctx.tiles)
+        return dq, dk, dv, None, None
+
+
+def fused_attention_autograd(q, k, v, tile_m=64, tile_n=64):
+    """Causal attention (B, H, N, D) float16/bfloat16 with autograd support."""
+    return FusedAttentionFn.apply(q, k, v, tile_m, tile_n)

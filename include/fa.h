@@ -1,0 +1,94 @@
+/*
+ * fa.h - C ABI of libfa.so, the MI355X (gfx950) fused causal attention library.
+ *
+ * Every entry point enqueues work on the caller's HIP stream and returns
+ * without synchronising.  The caller owns every buffer (inputs, outputs and
+ * LSE); the library allocates no device memory and keeps no pointer after
+ * a call returns.  All tensors are dense, row-major [B, heads, S, D] in
+ * device memory; LSE is dense [B, H, S] float32.
+ *
+ * Return value: FA_OK (0) or one of the negative FA_ERR_* codes below.
+ * fa_strerror() turns a code into a static message.
+ */
+#ifndef FA_H
+#define FA_H
+
+#if defined(__GNUC__) || defined(__clang__)
+#define FA_API __attribute__((visibility("default")))
+#else
+#define FA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum fa_dtype { FA_F16 = 0, FA_BF16 = 1 };
+
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_DIMS = -1,     /* B, H, H_kv or S not positive, or H % H_kv != 0 */
+  FA_ERR_DTYPE = -2,    /* dtype is neither FA_F16 nor FA_BF16 */
+  FA_ERR_HEADDIM = -3,  /* D not in {32, 64, 128} */
+  FA_ERR_TILE = -4,     /* block_m / block_n not in {64, 128} or not dividing S */
+  FA_ERR_NULL = -5,     /* a required pointer is NULL */
+  FA_ERR_LAUNCH = -6,   /* the HIP runtime rejected a launch */
+  FA_ERR_UNSUPPORTED = -7 /* valid arguments, but no kernel for this combination */
+};
+
+/*
+ * Causal forward O = softmax(Q K^T / sqrt(D) + causal mask) V, optionally
+ * writing the per-row log-sum-exp.
+ *
+ * Replaces the device launch of:
+ *   attention/fused/fused.py:68-76        fused_attention          (H_kv == H, lse NULL)
+ *   attention/gqa/fused_gqa.py:70-82      fused_gqa_attention      (H_kv divides H, lse NULL)
+ *   attention/backward/fused_backward.py:161-170  _forward         (H_kv == H, lse non-NULL)
+ *
+ * q, o : [B, H, S, D]      k, v : [B, H_kv, S, D]     element type = dtype
+ * lse  : NULL, or [B, H, S] float32 receiving m + log2(l): the base-2 log-sum-exp
+ *        of the scores pre-multiplied by scale_log2 (the quantity the reference
+ *        builds at attention/backward/fused_backward.py:169).
+ * scale_log2 : log2(e) / sqrt(D) as the reference folds it (fused.py:74).
+ * Query head h reads K/V head h / (H / H_kv) (fused_gqa.py:18).
+ * block_m / block_n : query rows per head and keys per LDS tile, each in {64, 128},
+ *        each dividing S (the reference's tile_m / tile_n contract, fused.py:70-71).
+ */
+FA_API int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+           int B, int H, int H_kv, int S, int D, int dtype, float scale_log2,
+           int block_m, int block_n, void* hip_stream);
+
+/*
+ * Recompute backward of the causal forward: dQ, dK, dV from Q, K, V, O, dO and
+ * the LSE written by fa_fwd.  Two atomic-free kernels run in order on the stream:
+ * dK/dV (one workgroup per key tile) then dQ (one workgroup per query tile).
+ * Delta = rowsum(dO * O) is computed inside both kernels; no workspace.
+ *
+ * Replaces attention/backward/fused_backward.py:173-184 (_backward: the torch
+ * Delta op at :175 and the two launches at :180-183).
+ *
+ * q, k, v, o, d_o, dq, dk, dv : [B, H, S, D] (MHA, as the reference's _check
+ * requires at fused_backward.py:154); lse : [B, H, S] float32 from fa_fwd.
+ * sm_scale = 1/sqrt(D) scales dQ and dK once at the end (fused_backward.py:105,146).
+ */
+FA_API int fa_bwd(const void* q, const void* k, const void* v, const void* o,
+           const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+           int B, int H, int S, int D, int dtype, float scale_log2, float sm_scale,
+           int block_m, int block_n, void* hip_stream);
+
+/* 1 if a forward (with_lse 0/1) or backward (is_bwd 1) kernel exists for the
+ * combination, else 0.  No reference counterpart: it lets a caller probe the
+ * supported (dtype, D, tile) set before validating inputs. */
+FA_API int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with_lse, int is_bwd);
+
+/* Static, NUL-terminated description of a status code. */
+FA_API const char* fa_strerror(int status);
+
+/* Library version as 10000*major + 100*minor + patch. */
+FA_API int fa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_H */

@@ -1,0 +1,108 @@
+"""The C ABI of libfa.so, checked without a GPU.
+
+The library must load, export every function include/fa.h declares, and reject
+bad arguments with the documented status codes before touching the device.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from attention import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "fa.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_signatures():
+    assert header_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_header_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.fa_version() >= 100
+
+
+def test_no_internal_symbols_leak():
+    out = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert {"fa_fwd", "fa_bwd", "fa_supported", "fa_strerror", "fa_version"} <= exported
+    assert not any(s.startswith("fa_fwd_table") or s.startswith("fa_bwd_table") for s in exported)
+
+
+def test_strerror_covers_every_status(lib):
+    for code in range(0, -8, -1):
+        assert lib.fa_strerror(code).decode() not in ("", "unknown status")
+    assert lib.fa_strerror(-99).decode() == "unknown status"
+
+
+NULL = ctypes.c_void_p(0)
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every case below fails validation first
+
+
+def fwd(lib, B=1, H=2, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE, lse=NULL):
+    return lib.fa_fwd(ptr, ptr, ptr, ptr, lse, B, H, Hkv, S, D, dtype, 0.1, bm, bn, NULL)
+
+
+def bwd(lib, B=1, H=2, S=256, D=64, dtype=0, bm=64, bn=64, ptr=FAKE):
+    return lib.fa_bwd(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, B, H, S, D, dtype, 0.1, 0.1, bm, bn, NULL)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=0), _lib.FA_ERR_DIMS),
+    (dict(S=-64), _lib.FA_ERR_DIMS),
+    (dict(Hkv=3), _lib.FA_ERR_DIMS),
+    (dict(Hkv=4), _lib.FA_ERR_DIMS),
+    (dict(dtype=2), _lib.FA_ERR_DTYPE),
+    (dict(D=48), _lib.FA_ERR_HEADDIM),
+    (dict(D=256), _lib.FA_ERR_HEADDIM),
+    (dict(bm=32), _lib.FA_ERR_TILE),
+    (dict(bn=256), _lib.FA_ERR_TILE),
+    (dict(S=192, bm=128), _lib.FA_ERR_TILE),
+    (dict(ptr=NULL), _lib.FA_ERR_NULL),
+])
+def test_fwd_rejects_bad_arguments(lib, kw, code):
+    assert fwd(lib, **kw) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=0), _lib.FA_ERR_DIMS),
+    (dict(dtype=7), _lib.FA_ERR_DTYPE),
+    (dict(D=96), _lib.FA_ERR_HEADDIM),
+    (dict(S=320, bn=128), _lib.FA_ERR_TILE),
+    (dict(ptr=NULL), _lib.FA_ERR_NULL),
+])
+def test_bwd_rejects_bad_arguments(lib, kw, code):
+    assert bwd(lib, **kw) == code
+
+
+def test_supported_table(lib):
+    for dtype in (0, 1):
+        for D in (32, 64, 128):
+            for bm in (64, 128):
+                for bn in (64, 128):
+                    assert lib.fa_supported(dtype, D, bm, bn, 1, 0, 0) == 1
+                    assert lib.fa_supported(dtype, D, bm, bn, 1, 1, 0) == 1
+                    for group in (2, 4, 8, 32):
+                        assert lib.fa_supported(dtype, D, bm, bn, group, 0, 0) == 1
+    assert lib.fa_supported(1, 128, 64, 64, 0, 0, 0) == 0
+    assert lib.fa_supported(1, 96, 64, 64, 1, 0, 0) == 0
+
+
+def test_error_mapping_to_reference_exceptions():
+    with pytest.raises(TypeError):
+        _lib.check(_lib.FA_ERR_DTYPE, "x")
+    for code in (_lib.FA_ERR_DIMS, _lib.FA_ERR_HEADDIM, _lib.FA_ERR_TILE, _lib.FA_ERR_UNSUPPORTED):
+        with pytest.raises(ValueError):
+            _lib.check(code, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.FA_ERR_LAUNCH, "x")
+    _lib.check(_lib.FA_OK, "x")
