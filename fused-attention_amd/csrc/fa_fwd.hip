@@ -11,59 +11,96 @@
 //     l = l*alpha + rowsum(p)       (unrounded p)
 //     acc = acc*alpha + p(rounded to the input type) . v
 //   O = acc / l; optional LSE = m + log2(l) (fused_backward.py:169).
+// The rescale of acc and l is skipped for a tile when no row of the wave has a
+// new maximum (alpha would be exactly 1).  FA_RESCALE_THRESHOLD > 0 widens the
+// skip to max increases below that many powers of two (p then stays <= 2^T);
+// O = acc / l and LSE = m + log2(l) do not depend on the reference point, but
+// a dominant p is then no longer exactly 1 before its rounding to 16 bits, so
+// the default threshold is 0.
 //
 // MI355X mapping:
 //   * one workgroup = GH query heads (sharing one K/V head) x BM query rows;
 //     one wave = one head x 32 query rows; WR = BM/32 waves per head.
 //   * each wave computes S^T = K Q^T (keys x queries) so a lane owns ONE query
 //     row: row max / row sum are register-local plus one permlane32 swap, and the
-//     accumulator is fed straight back as the B operand of O^T += V^T P^T.
-//   * Q stays in registers for the whole loop; K (row-major) and V^T
-//     (transposed on the LDS write) tiles are double-buffered in LDS; the next
-//     tile's global loads are in flight while the current tile is computed.
+//     score accumulator is fed straight back as the B operand of O^T += V^T P^T.
+//   * Q stays in registers for the whole loop.  K and V tiles go global -> LDS
+//     with global_load_lds_dwordx4 (no VGPR staging), double-buffered in two
+//     LDS arrays; the next tile's DMA runs while the current tile is computed.
+//   * V^T operands come from ds_read_b64_tr_b16 on the row-major V tile, so no
+//     transpose is ever materialised.
 //   * causal skipping at two levels: key tiles past the workgroup's last row are
-//     never loaded, and each wave skips 32-key blocks past its own last row.
+//     never loaded, and each wave skips 32-key blocks past its own last row;
+//     tiles wholly below the diagonal run a mask-free path.
 //   * heavy-first, XCD-aware order: the 8 XCDs each take a contiguous range of
 //     (batch, head-group) units; inside a unit the last (heaviest) query tile
 //     is dispatched first.
+//
+// LDS layouts (one buffer = K tile then V tile, each BN rows x D, row-major):
+//   K: 16-byte chunk ch of row r stored at chunk ch ^ (r & 7); an MFMA A-operand
+//      read (lane c reads row c, one chunk) then hits 8 distinct bank groups per
+//      8 lanes.
+//   V: byte b of row r stored at b ^ (32 * (r & 3)); a transposed read (16 lanes
+//      = 4 rows x 32 bytes) then hits 4 distinct 32-byte bank groups.
 #include "fa_device.h"
 #include "fa_launch.h"
 
 namespace fa {
 
-// Two waves per SIMD where the working set fits 256 VGPRs without spilling
-// (64-key tiles with >= 4 waves per workgroup), otherwise one.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+constexpr int kWaitVmcnt0 = 0x0F70;
+// skip the rescale unless a row max grows by more than this (log2 units)
+#ifndef FA_RESCALE_THRESHOLD
+#define FA_RESCALE_THRESHOLD 0.0f
+#endif
+constexpr float kRescaleThreshold = FA_RESCALE_THRESHOLD;
+
 template <int D, int BM, int BN, int GH>
 constexpr int fwd_waves_per_simd() {
   return (BN == 64 && (BM / 32) * GH >= 4) ? 2 : 1;
 }
 
+template <bool B>
+struct Tag {
+  static constexpr bool value = B;
+};
+
+// Two 8-byte transposed LDS reads -> one 16-byte MFMA operand.
+__device__ __forceinline__ u32x4 lds_read_tr16x2(const unsigned char* base, int off0, int off1) {
+  i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + off0));
+  i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + off1));
+  u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
 template <typename E, int D, int BM, int BN, int GH, bool LSE>
 __global__ __launch_bounds__(64 * (BM / 32) * GH)
 __attribute__((amdgpu_waves_per_eu(fwd_waves_per_simd<D, BM, BN, GH>(), fwd_waves_per_simd<D, BM, BN, GH>())))
-void fwd_kernel(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse,
-    int B, int H, int Hkv, int S, float scale_log2) {
+void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse,
+                int B, int H, int Hkv, int S, float scale_log2) {
   constexpr int WR = BM / 32;
-  constexpr int NT = 64 * WR * GH;
-  constexpr int KCH = D / 8;                      // 16-byte chunks per K row
-  constexpr int NB = BN / 32;                     // 32-key blocks per tile
-  constexpr int KT = D / 16;                      // MFMA k-steps over D
-  constexpr int DB = D / 32;                      // 32-row blocks of O^T
-  constexpr int K_BYTES = BN * D * 2;
-  constexpr int V_BYTES = D * BN * 2;
-  constexpr int BUF_BYTES = K_BYTES + V_BYTES;
-  constexpr int K_ITEMS = BN * KCH;               // 16-byte chunks per K tile
-  constexpr int V_ITEMS = (BN / 4) * (D / 8);     // 4x8 items per V tile
-  constexpr int K_PER = (K_ITEMS + NT - 1) / NT;
-  constexpr int V_PER = (V_ITEMS + NT - 1) / NT;
+  constexpr int NW = WR * GH;
+  constexpr int NB = BN / 32;          // 32-key blocks per tile
+  constexpr int KT = D / 16;           // MFMA k-steps over D
+  constexpr int DB = D / 32;           // 32-row blocks of O^T
+  constexpr int ROWB = D * 2;          // bytes per K/V row
+  constexpr int TILE = BN * ROWB;      // bytes per K or V tile
+  constexpr int NBLK = TILE / 1024;    // 1 KB DMA blocks per tile
+  constexpr int CPR = ROWB / 16;       // 16-byte chunks per row
+  constexpr int KMASK = (CPR >= 8 ? 8 : CPR) - 1;
+  static_assert(TILE % 1024 == 0, "tile must be whole 1 KB DMA blocks");
   const float NEG_INF = -__builtin_inff();
 
-  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * TILE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
   const int wh = wave % GH, wr = wave / GH;
 
@@ -80,13 +117,38 @@ void fwd_kernel(
   const int hq = h0 + wh;
   const int hkv = h0 / (H / Hkv);
 
-  const uint16_t* Kbh = K + (size_t)(b * Hkv + hkv) * S * D;
-  const uint16_t* Vbh = V + (size_t)(b * Hkv + hkv) * S * D;
+  const unsigned char* Kbh = reinterpret_cast<const unsigned char*>(K + (size_t)(b * Hkv + hkv) * S * D);
+  const unsigned char* Vbh = reinterpret_cast<const unsigned char*>(V + (size_t)(b * Hkv + hkv) * S * D);
   const size_t qbase = (size_t)(b * H + hq) * S * D;
 
   const int r0 = qt * BM;          // first query row of this workgroup
   const int q0 = r0 + wr * 32;     // first query row of this wave
   const int m = q0 + c;            // this lane's query row
+  const int ntiles = (r0 + BM + BN - 1) / BN;
+  const int jfull = r0 / BN;       // tiles wholly below the workgroup's first row
+
+  // ---- DMA of one K/V tile into an LDS buffer: 1 KB per wave instruction,
+  // lane L's 16 bytes land at block + 16 L; the lane loads the global bytes
+  // that belong there under the swizzles above.
+  const int drow = lane / CPR;                 // row inside a 1 KB block
+  const int dpos = (lane % CPR) * 16;          // LDS byte offset inside the row
+  auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+    const unsigned char* Kt = Kbh + (size_t)j * TILE;
+    const unsigned char* Vt = Vbh + (size_t)j * TILE;
+#pragma unroll
+    for (int i = 0; i < (NBLK + NW - 1) / NW; ++i) {
+      const int blk = wave + i * NW;
+      if (NBLK % NW == 0 || blk < NBLK) {
+        const int row = blk * (1024 / ROWB) + drow;
+        const int kpos = (((dpos >> 4) ^ (row & KMASK)) << 4);
+        const int vpos = dpos ^ ((32 * (row & 3)) & (ROWB - 1));
+        __builtin_amdgcn_global_load_lds(Kt + row * ROWB + kpos,
+                                         (__attribute__((address_space(3))) void*)(buf + blk * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(Vt + row * ROWB + vpos,
+                                         (__attribute__((address_space(3))) void*)(buf + TILE + blk * 1024), 16, 0, 0);
+      }
+    }
+  };
 
   // ---- Q^T operand in registers: k-step t holds Q[m][16t + 8hh .. +7]
   u32x4 qf[KT];
@@ -95,158 +157,151 @@ void fwd_kernel(
 #pragma unroll
     for (int t = 0; t < KT; ++t) qf[t] = gload16(qrow + 16 * t);
   }
+  dma_tile(0, lds0);
+
+  // ---- per-lane LDS operand offsets
+  // K A-operand, k-step t: row c, chunk (2t+hh) ^ (c & KMASK) -> koff[t&3] + 128*(t>>2)
+  int koff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) koff[t] = c * ROWB + ((((2 * t + hh) & (CPR - 1)) ^ (c & KMASK)) << 4);
+  // V^T A-operand via transposed reads: in 16-lane group G, lane (kr, c4) addresses
+  // key row 4hh + kr (+ block offsets) and the 4 columns feeding output lanes
+  // 4c4..4c4+3, which hold d = pi(16(G&1) + 4c4) + 0..3 of the 32-d block.
+  int voff_even, voff_odd;
+  {
+    const int G = lane >> 4, kr = (lane >> 2) & 3, c4 = lane & 3;
+    const int e = 2 * pi_swap23(16 * (G & 1) + 4 * c4);     // byte offset < 64
+    const int k1 = (ROWB >= 128) ? (kr >> 1) : 0;
+    const int base = (4 * hh + kr) * ROWB + (e ^ (32 * (kr & 1)));
+    voff_even = base + 64 * k1;           // (64 db + e) ^ 32 kr for even db, minus 64 db
+    voff_odd = base + 64 * (1 - k1) - 64;  // same for odd db
+  }
 
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
   float mrun = NEG_INF, lrun = 0.f;
 
-  const int ntiles = (r0 + BM + BN - 1) / BN;
-
-  // ---- global -> register prefetch of one K/V tile
-  u32x4 kpre[K_PER];
-  u32x4 vpre[V_PER][4];
-  auto load_tile = [&](int j) {
-    const uint16_t* Kt = Kbh + (size_t)j * BN * D;
-    const uint16_t* Vt = Vbh + (size_t)j * BN * D;
-#pragma unroll
-    for (int it = 0; it < K_PER; ++it) {
-      const int i = tid + it * NT;
-      if (K_ITEMS % NT == 0 || i < K_ITEMS) kpre[it] = gload16(Kt + (size_t)i * 8);
+  // ---- one key tile
+  auto compute = [&](const unsigned char* Ks, int k0, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(mask_tag)::value;
+    const unsigned char* Vs = Ks + TILE;
+    int nvalid = NB;
+    if constexpr (MASKED) {
+      nvalid = (q0 + 32 - k0) / 32;
+      nvalid = nvalid > NB ? NB : nvalid;
+      if (nvalid <= 0) return;
     }
+
+    // S^T = K Q^T: A row c <- key 32nb + c; register g of lane (c, hh) holds
+    // key offset 8*(g/4) + 4*hh + (g%4) of the block, query c
+    f32x16 s[NB];
 #pragma unroll
-    for (int it = 0; it < V_PER; ++it) {
-      const int i = tid + it * NT;
-      if (V_ITEMS % NT == 0 || i < V_ITEMS) {
-        int g, cc;
-        tr_item<D>(i, g, cc);
+    for (int nb = 0; nb < NB; ++nb) {
+      if (!MASKED || nb < nvalid) {
+        f32x16 x = f32x16{};
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          vpre[it][rr] = gload16(Vt + (size_t)(4 * g + rr) * D + 8 * cc);
+        for (int t = 0; t < KT; ++t)
+          x = mfma32<E>(lds_read16(Ks, koff[t & 3] + 128 * (t >> 2) + nb * 32 * ROWB), qf[t], x);
+        s[nb] = x;
       }
     }
-  };
-  auto store_tile = [&](int buf) {
-    unsigned char* Ks = smem + buf * BUF_BYTES;
-    unsigned char* Vs = Ks + K_BYTES;
-#pragma unroll
-    for (int it = 0; it < K_PER; ++it) {
-      const int i = tid + it * NT;
-      if (K_ITEMS % NT == 0 || i < K_ITEMS) lds_write16(Ks, rm_off<D>(i / KCH, i % KCH), kpre[it]);
-    }
-#pragma unroll
-    for (int it = 0; it < V_PER; ++it) {
-      const int i = tid + it * NT;
-      if (V_ITEMS % NT == 0 || i < V_ITEMS) {
-        int g, cc;
-        tr_item<D>(i, g, cc);
-        tr_write<BN>(Vs, g, cc, vpre[it]);
-      }
-    }
-  };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int j = 0; j < ntiles; ++j) {
-    const int buf = j & 1;
-    const bool more = (j + 1 < ntiles);
-    if (more) load_tile(j + 1);
-
-    const int k0 = j * BN;
-    // 32-key blocks of this tile whose first key is <= the wave's last row
-    int nvalid = (q0 + 32 - k0) / 32;
-    nvalid = nvalid < 0 ? 0 : (nvalid > NB ? NB : nvalid);
-
-    if (nvalid > 0) {
-      const unsigned char* Ks = smem + buf * BUF_BYTES;
-      const unsigned char* Vs = Ks + K_BYTES;
-
-      // S^T = K Q^T, 32 keys per block; A row c <- key 32*nb + pi(c)
-      f32x16 s[NB];
+    float mx = NEG_INF;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        s[nb] = f32x16{};
-        if (nb < nvalid) {
-          const int key = nb * 32 + pi_swap23(c);
-#pragma unroll
-          for (int t = 0; t < KT; ++t) {
-            const u32x4 a = lds_read16(Ks, rm_off<D>(key, 2 * t + hh));
-            s[nb] = mfma32<E>(a, qf[t], s[nb]);
-          }
-        }
-      }
-
-      // causal mask on the diagonal block: register g holds key offset
-      // 16*(g/8) + 8*hh + (g%8) inside the block, the lane holds query c
-      float mx = NEG_INF;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        if (nb < nvalid) {
-          if (k0 + 32 * nb == q0) {
-#pragma unroll
-            for (int g = 0; g < 16; ++g) {
-              const int koff = 16 * (g >> 3) + 8 * hh + (g & 7);
-              if (koff > c) s[nb][g] = NEG_INF;
-            }
-          }
-#pragma unroll
-          for (int g = 0; g < 16; ++g) mx = fmaxf(mx, s[nb][g]);
-        }
-      }
-      mx = halfwave_max(mx);
-      const float mnew = fmaxf(mrun, mx * scale_log2);
-      const float alpha = fast_exp2(mrun - mnew);
-
-      // P^T packed as the B operand of the PV MFMAs: k-step u = 2*nb + i1
-      // holds keys 32nb + 16i1 + 8hh + 0..7
-      u32x4 pk[2 * NB];
-      float lsum = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        if (nb < nvalid) {
-          float p[16];
+    for (int nb = 0; nb < NB; ++nb) {
+      if (!MASKED || nb < nvalid) {
+        if (MASKED && k0 + 32 * nb == q0) {
 #pragma unroll
           for (int g = 0; g < 16; ++g) {
-            p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mnew));
-            lsum += p[g];
-          }
-#pragma unroll
-          for (int i1 = 0; i1 < 2; ++i1) {
-            u32x4 w;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
-            pk[2 * nb + i1] = w;
+            const int koffs = 8 * (g >> 2) + 4 * hh + (g & 3);
+            if (koffs > c) s[nb][g] = NEG_INF;
           }
         }
-      }
-      lrun = lrun * alpha + lsum;
-      mrun = mnew;
-
-      // O^T += V^T P^T; A row c <- d = 32*db + pi(c)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+        for (int g = 0; g < 16; ++g) mx = fmaxf(mx, s[nb][g]);
+      }
+    }
+    mx = halfwave_max(mx) * scale_log2;
+
+    // move the reference max (and rescale) only when some row's max grows
+    if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleThreshold)) {
+      const float mnew = fmaxf(mrun, mx);
+      const float alpha = fast_exp2(mrun - mnew);
+      mrun = mnew;
+      lrun *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int g = 0; g < 16; ++g) acc[db][g] *= alpha;
-        const int d = db * 32 + pi_swap23(c);
+    }
+
+    // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
+    // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7)
+    u32x4 pk[2 * NB];
+    float lsum = 0.f;
 #pragma unroll
-        for (int u = 0; u < 2 * NB; ++u) {
-          if ((u >> 1) < nvalid) {
-            const u32x4 a = lds_read16(Vs, tr_off<BN>(d, 2 * u + hh));
-            acc[db] = mfma32<E>(a, pk[u], acc[db]);
-          }
+    for (int nb = 0; nb < NB; ++nb) {
+      if (!MASKED || nb < nvalid) {
+        float p[16];
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+          p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
+          lsum += p[g];
+        }
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          u32x4 w;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+          pk[2 * nb + i1] = w;
         }
       }
     }
+    lrun += lsum;
 
-    if (more) {
-      store_tile(buf ^ 1);
-      __syncthreads();
+    // O^T += V^T P^T; operand rows are d = 32db + pi(row), keys per slot as above
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int vb = ((db & 1) ? voff_odd : voff_even) + 64 * db;
+#pragma unroll
+      for (int u = 0; u < 2 * NB; ++u) {
+        if (!MASKED || (u >> 1) < nvalid) {
+          const int o = vb + 16 * u * ROWB;
+          acc[db] = mfma32<E>(lds_read_tr16x2(Vs, o, o + 8 * ROWB), pk[u], acc[db]);
+        }
+      }
     }
+  };
+
+  auto step = [&](int j, auto par_tag, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool P = decltype(par_tag)::value;
+    unsigned char* cur = P ? lds1 : lds0;
+    unsigned char* nxt = P ? lds0 : lds1;
+    if (j + 1 < ntiles) dma_tile(j + 1, nxt);
+    compute(cur, j * BN, mask_tag);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+  };
+
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+
+  int j = 0;
+  for (; j + 1 < jfull; j += 2) {
+    step(j, Tag<false>{}, Tag<false>{});
+    step(j + 1, Tag<true>{}, Tag<false>{});
+  }
+  if (j < jfull) {
+    step(j, Tag<false>{}, Tag<false>{});
+    ++j;
+  }
+  for (; j < ntiles; ++j) {
+    if (j & 1) step(j, Tag<true>{}, Tag<true>{});
+    else step(j, Tag<false>{}, Tag<true>{});
   }
 
-  // ---- epilogue: O = acc / l, 16 contiguous bytes per lane per (db, i1)
+  // ---- epilogue: O = acc / l; lane holds d = 32db + 16i1 + 8hh + 0..7
   const float ltot = halfwave_sum(lrun);
   const float inv = 1.0f / ltot;
   uint16_t* orow = O + qbase + (size_t)m * D;
@@ -264,11 +319,8 @@ void fwd_kernel(
 template <typename E, int D, int BM, int BN, int GH, bool LSE>
 static int launch_fwd(const FwdArgs& a) {
   constexpr int NT = 64 * (BM / 32) * GH;
-  constexpr int SMEM = 2 * (BN * D * 2 + D * BN * 2);
-  auto kern = fwd_kernel<E, D, BM, BN, GH, LSE>;
-  if (!set_smem_once(reinterpret_cast<const void*>(kern), SMEM)) return FA_ERR_LAUNCH;
   const int total = a.B * (a.H / GH) * (a.S / BM);
-  hipLaunchKernelGGL(kern, dim3(total), dim3(NT), SMEM, (hipStream_t)a.stream,
+  hipLaunchKernelGGL((fwd_kernel<E, D, BM, BN, GH, LSE>), dim3(total), dim3(NT), 0, (hipStream_t)a.stream,
                      (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
                      (uint16_t*)a.o, a.lse, a.B, a.H, a.Hkv, a.S, a.scale_log2);
   return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
