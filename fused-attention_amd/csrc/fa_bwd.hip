@@ -1,8 +1,522 @@
-// fa_bwd.hip - placeholder table until the backward kernels land.
+// fa_bwd.hip - atomic-free recompute backward of causal attention for gfx950.
+//
+// Math (attention/backward/fused_backward.py:66-147, report p.10 eq. 5), per (b, h):
+//   P  = exp2(S*c - LSE)     with S = Q K^T, c = log2(e)/sqrt(D), LSE from the forward
+//   dV = P^T dO              dP = dO V^T        Delta = rowsum(dO * O)
+//   dS = P * (dP - Delta)    dQ = dS K / sqrt(D)  dK = dS^T Q / sqrt(D)
+// Two kernels, launched in this order on the caller's stream:
+//   dkdv_kernel: one workgroup per key tile (tile_n keys, 32 per wave); loops over
+//                the query tiles (tile_m rows) at and below the diagonal.  Per query
+//                tile, Q, dO, O and LSE are copied global -> LDS by DMA (double
+//                buffered) and Delta is formed from the O and dO tiles in LDS.
+//                Each wave keeps its K and V rows in registers as MFMA B operands,
+//                computes S = Q K^T and dP = dO V^T with one lane per key, and
+//                accumulates dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and
+//                Q^T with ds_read_b64_tr_b16.
+//   dq_kernel:   one workgroup per query tile (tile_m rows, 32 per wave); loops over
+//                the key tiles (tile_n keys) up to the diagonal, heavy first.  Each
+//                wave keeps Q and dO rows in registers, computes S^T = K Q^T and
+//                dP^T = V dO^T with one lane per query (LSE and Delta are per-lane
+//                scalars; Delta comes from the O and dO rows in the prologue) and
+//                accumulates dQ^T += K^T dS^T, reading K^T with transposed reads.
+// Neither kernel uses atomics or a workspace; each output element is written once.
+//
+// LDS tiles are row-major with 16-byte chunk ch of row r stored at
+// ch ^ bswz(r), bswz(r) = 2*(r & 3) + ((r >> 2) & 1): 8 consecutive rows read at
+// one chunk hit 8 distinct bank groups (MFMA operand reads), and 4 consecutive
+// rows read as 32-byte pieces (transposed reads) hit 4 distinct 32-byte groups.
 #include "fa_device.h"
 #include "fa_launch.h"
 
-extern "C" FA_HIDDEN fa::BwdFn FA_BWD_TABLE(int bm, int bn) {
-  (void)bm; (void)bn;
+namespace fa {
+
+typedef short i16x4b __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4b lds_i16x4b;
+
+constexpr int kBwdWaitVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0)
+
+template <bool B>
+struct BTag {
+  static constexpr bool value = B;
+};
+
+// Chunk swizzle of row r for rows of cpr 16-byte chunks.  A plain function (not a
+// template): a template call inside the LDS-DMA builtin's operands keeps clang
+// from emitting the kernel's host-side launch stub.
+__host__ __device__ __forceinline__ int bswz(int r, int cpr) {
+  return ((((r & 3) << 1) | ((r >> 2) & 1))) & ((cpr >= 8 ? 8 : cpr) - 1);
+}
+
+__device__ __forceinline__ u32x4 tr_read2(const unsigned char* base, int off0, int off1) {
+  i16x4b a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4b*)(base + off0));
+  i16x4b b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4b*)(base + off1));
+  u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
+// Per-lane offsets into a swizzled row-major tile with rows of ROWB bytes.
+//  opnd[t&3] + 128*(t>>2): MFMA operand read, lane c -> row c, chunk 2t + hh
+//  tr_even / tr_odd + 64*db + (16u + 8r2)*ROWB: transposed read feeding an A
+//    operand whose rows are d = 32db + pi(lane % 32) and whose k-slots are rows
+//    16u + 8*r2 + 4*hh + (0..3) of the tile (the slot order of a score
+//    accumulator used as the B operand)
+template <int ROWB>
+struct TileOffsets {
+  int opnd[4];
+  int tr_even, tr_odd;
+  __device__ __forceinline__ void init(int lane) {
+    constexpr int CPR = ROWB / 16;
+    const int c = lane & 31, hh = lane >> 5;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) opnd[t] = c * ROWB + ((((2 * t + hh) & (CPR - 1)) ^ bswz(c, CPR)) << 4);
+    const int G = lane >> 4, kr = (lane >> 2) & 3, c4 = lane & 3;
+    const int x = (2 * pi_swap23(16 * (G & 1) + 4 * c4)) >> 4;  // chunk 0..3 of the 64-byte d range
+    const int within = (2 * pi_swap23(16 * (G & 1) + 4 * c4)) & 8;
+    const int sl = bswz(4 * hh + kr, CPR);                        // swizzle of every row this lane reads
+    const int k1 = (CPR >= 8) ? (sl >> 2) : 0;
+    const int base = (4 * hh + kr) * ROWB + ((x ^ (sl & 3)) << 4) + within;
+    tr_even = base + 64 * k1;
+    tr_odd = base + 64 * (1 - k1) - 64;
+  }
+  __device__ __forceinline__ int tr(int db, int u, int r2) const {
+    return ((db & 1) ? tr_odd : tr_even) + 64 * db + (16 * u + 8 * r2) * ROWB;
+  }
+};
+
+// Score-accumulator element (lane c, hh, register g) -> row offset inside a 32-row block.
+__host__ __device__ __forceinline__ int acc_row(int g, int hh) { return 8 * (g >> 2) + 4 * hh + (g & 3); }
+
+// ===========================================================================
+// dK / dV
+// ===========================================================================
+template <typename E, int D, int BMQ, int BNK>
+__global__ __launch_bounds__(2 * BNK)
+__attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1)))
+void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                 const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
+                 const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
+                 uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+                 int B, int H, int S, float scale_log2, float sm_scale) {
+  constexpr int NW = BNK / 32;
+  constexpr int NT = 64 * NW;
+  constexpr int KT = D / 16, DB = D / 32, QB = BMQ / 32;
+  constexpr int ROWB = D * 2, CPR = ROWB / 16;
+  constexpr int TILE = BMQ * ROWB;              // bytes of one Q / dO / O tile
+  constexpr int NBLK = TILE / 1024;
+  constexpr int BUF = 3 * TILE + BMQ * 4;       // Q | dO | O | LSE
+  constexpr int TPR = NT / BMQ;                 // threads per row for Delta
+  static_assert(TILE % 1024 == 0, "tiles are whole 1 KB DMA blocks");
+  static_assert(TPR >= 1 && (CPR % TPR) == 0, "Delta split");
+  const float NEG_INF = -__builtin_inff();
+
+  __shared__ __attribute__((aligned(1024))) unsigned char buf0[BUF];
+  __shared__ __attribute__((aligned(1024))) unsigned char buf1[BUF];
+  __shared__ __attribute__((aligned(16))) float delta_s[BMQ];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, hh = lane >> 5;
+
+  // work item: (b, h, key tile), heaviest key tile (j = 0) first, XCD aware
+  const int nk = S / BNK;
+  const int total = B * H * nk;
+  const int wg = blockIdx.x;
+  const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
+  const int bh = L / nk, jt = L % nk;
+  const size_t base = (size_t)bh * S * D;
+  const unsigned char* Qb = reinterpret_cast<const unsigned char*>(Q + base);
+  const unsigned char* dOb = reinterpret_cast<const unsigned char*>(dO + base);
+  const unsigned char* Ob = reinterpret_cast<const unsigned char*>(O + base);
+  const float* Lb = Lse + (size_t)bh * S;
+
+  const int k0w = jt * BNK + 32 * wave;   // first key of this wave
+  const int n = k0w + c;                  // this lane's key
+
+
+  // K, V rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
+  u32x4 kf[KT], vf[KT];
+  {
+    const uint16_t* kr = K + base + (size_t)n * D + 8 * hh;
+    const uint16_t* vr = V + base + (size_t)n * D + 8 * hh;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      kf[t] = gload16(kr + 16 * t);
+      vf[t] = gload16(vr + 16 * t);
+    }
+  }
+
+  const int nq = S / BMQ;
+  const int i0 = (jt * BNK) / BMQ;        // first query tile that sees this key tile
+
+  // DMA of the Q, dO and O tiles (row-major, swizzled) and the LSE slice of query
+  // tile i into an LDS buffer: waves take 1 KB blocks round-robin and lane L of a
+  // block writes LDS bytes blk*1024 + 16L.
+  const int drow = lane / CPR, dch = lane % CPR;
+  auto dma_tile = [&](int i, unsigned char* buf) __attribute__((always_inline)) {
+    const size_t off = (size_t)i * TILE;
+#pragma unroll
+    for (int part = 0; part < 3; ++part) {
+      const unsigned char* g = (part == 0 ? Qb : (part == 1 ? dOb : Ob)) + off;
+#pragma unroll
+      for (int x = 0; x < (NBLK + NW - 1) / NW; ++x) {
+        const int blk = wave + x * NW;
+        if (NBLK % NW == 0 || blk < NBLK) {
+          const int row = blk * (1024 / ROWB) + drow;
+          __builtin_amdgcn_global_load_lds(g + row * ROWB + ((dch ^ bswz(row, CPR)) << 4),
+                                           (__attribute__((address_space(3))) void*)(buf + part * TILE + blk * 1024),
+                                           16, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < (BMQ + 63) / 64; ++p) {
+      if (wave == p % NW && 64 * p + lane < BMQ)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned char*>(Lb + (size_t)i * BMQ + 64 * p + lane),
+                                         (__attribute__((address_space(3))) void*)(buf + 3 * TILE + 256 * p), 4, 0, 0);
+    }
+  };
+
+  TileOffsets<ROWB> to;
+  to.init(lane);
+
+  f32x16 dv_acc[DB], dk_acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dv_acc[db] = f32x16{};
+    dk_acc[db] = f32x16{};
+  }
+
+  // Delta for the tile in `buf`: TPR threads per row, chunk subsets, then shuffles
+  auto delta_phase = [&](const unsigned char* buf) __attribute__((always_inline)) {
+    const int row = tid / TPR, part = tid % TPR;
+    float acc = 0.f;
+#pragma unroll
+    for (int x = 0; x < CPR / TPR; ++x) {
+      const int ch = part + TPR * x;
+      const int off = row * ROWB + ((ch ^ bswz(row, CPR)) << 4);
+      const u32x4 a = lds_read16(buf + TILE, off);
+      const u32x4 o = lds_read16(buf + 2 * TILE, off);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        acc += to_f32<E>(a[w] & 0xFFFFu) * to_f32<E>(o[w] & 0xFFFFu);
+        acc += to_f32<E>(a[w] >> 16) * to_f32<E>(o[w] >> 16);
+      }
+    }
+#pragma unroll
+    for (int sh = 1; sh < TPR; sh <<= 1) acc += __shfl_xor(acc, sh, 64);
+    if (part == 0) delta_s[row] = acc;
+  };
+
+  auto compute = [&](const unsigned char* buf, int qtile0) __attribute__((always_inline)) {
+    const unsigned char* Qs = buf;
+    const unsigned char* dOs = buf + TILE;
+    const float* Ls = reinterpret_cast<const float*>(buf + 3 * TILE);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qrow0 = qtile0 + 32 * qb;   // first query of this block
+      if (qrow0 + 31 < k0w) continue;       // every query precedes every key of the wave
+      // S = Q K^T and dP = dO V^T: lane (c = key, hh), register g -> query qrow0 + acc_row(g)
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int o = to.opnd[t & 3] + 128 * (t >> 2) + 32 * qb * ROWB;
+        s = mfma32<E>(lds_read16(Qs, o), kf[t], s);
+        dp = mfma32<E>(lds_read16(dOs, o), vf[t], dp);
+      }
+      float lse[16], dl[16];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int r = 32 * qb + 8 * gq + 4 * hh;
+        const f32x4 lv = *reinterpret_cast<const f32x4*>(Ls + r);
+        const f32x4 dv = *reinterpret_cast<const f32x4*>(delta_s + r);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lse[4 * gq + e] = lv[e];
+          dl[4 * gq + e] = dv[e];
+        }
+      }
+      const bool diag = (qrow0 == k0w);
+      float p[16], ds[16];
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        float x = s[g];
+        if (diag && c > acc_row(g, hh)) x = NEG_INF;
+        p[g] = fast_exp2(__builtin_fmaf(x, scale_log2, -lse[g]));
+        ds[g] = p[g] * (dp[g] - dl[g]);
+      }
+      u32x4 pk[2], dsk[2];
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          pk[i1][q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+          dsk[i1][q] = pack2<E>(ds[8 * i1 + 2 * q], ds[8 * i1 + 2 * q + 1]);
+        }
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS (k-slots: queries 32qb + 16i1 + 8r2 + 4hh + 0..3)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const int u = 2 * qb + i1;
+          dv_acc[db] = mfma32<E>(tr_read2(dOs, to.tr(db, u, 0), to.tr(db, u, 1)), pk[i1], dv_acc[db]);
+          dk_acc[db] = mfma32<E>(tr_read2(Qs, to.tr(db, u, 0), to.tr(db, u, 1)), dsk[i1], dk_acc[db]);
+        }
+      }
+    }
+  };
+  // ---- main loop over query tiles i0 .. nq-1
+  auto step = [&](int i, auto par_tag) __attribute__((always_inline)) {
+    constexpr bool P = decltype(par_tag)::value;
+    unsigned char* cur = P ? buf1 : buf0;
+    unsigned char* nxt = P ? buf0 : buf1;
+    if (i + 1 < nq) dma_tile(i + 1, nxt);
+    delta_phase(cur);
+    __syncthreads();
+    compute(cur, i * BMQ);
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+  };
+
+  dma_tile(i0, buf0);
+  __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+  __syncthreads();
+  int i = i0;
+  for (; i + 1 < nq; i += 2) {
+    step(i, BTag<false>{});
+    step(i + 1, BTag<true>{});
+  }
+  if (i < nq) step(i, BTag<false>{});
+
+  // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7
+  uint16_t* dkr = dK + base + (size_t)n * D;
+  uint16_t* dvr = dV + base + (size_t)n * D;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1) {
+      gstore16(dkr + db * 32 + 16 * i1 + 8 * hh, pack8<E>(dk_acc[db], 8 * i1, sm_scale));
+      gstore16(dvr + db * 32 + 16 * i1 + 8 * hh, pack8<E>(dv_acc[db], 8 * i1, 1.0f));
+    }
+  }
+}
+
+// ===========================================================================
+// dQ
+// ===========================================================================
+template <typename E, int D, int BM, int BN>
+__global__ __launch_bounds__(2 * BM)
+__attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1)))
+void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+               const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
+               const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
+               uint16_t* __restrict__ dQ, int B, int H, int S, float scale_log2, float sm_scale) {
+  constexpr int NW = BM / 32;
+  constexpr int NB = BN / 32, KT = D / 16, DB = D / 32;
+  constexpr int ROWB = D * 2, CPR = ROWB / 16;
+  constexpr int TILE = BN * ROWB;
+  constexpr int NBLK = TILE / 1024;
+  static_assert(TILE % 1024 == 0, "tiles are whole 1 KB DMA blocks");
+  const float NEG_INF = -__builtin_inff();
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * TILE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, hh = lane >> 5;
+
+  // work item: (b, h, query tile), heaviest (last) query tile first, XCD aware
+  const int nq = S / BM;
+  const int total = B * H * nq;
+  const int wg = blockIdx.x;
+  const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
+  const int bh = L / nq, qt = nq - 1 - (L % nq);
+  const size_t base = (size_t)bh * S * D;
+  const unsigned char* Kb = reinterpret_cast<const unsigned char*>(K + base);
+  const unsigned char* Vb = reinterpret_cast<const unsigned char*>(V + base);
+
+  const int r0 = qt * BM, q0 = r0 + 32 * wave, m = q0 + c;
+  const int ntiles = (r0 + BM + BN - 1) / BN;
+  const int jfull = r0 / BN;
+
+
+  // Q and dO rows as B operands; Delta = rowsum(dO * O) from the same row halves
+  u32x4 qf[KT], dof[KT];
+  float delta;
+  {
+    const uint16_t* qr = Q + base + (size_t)m * D + 8 * hh;
+    const uint16_t* dr = dO + base + (size_t)m * D + 8 * hh;
+    const uint16_t* orr = O + base + (size_t)m * D + 8 * hh;
+    float part = 0.f;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      qf[t] = gload16(qr + 16 * t);
+      dof[t] = gload16(dr + 16 * t);
+      const u32x4 o = gload16(orr + 16 * t);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        part += to_f32<E>(dof[t][w] & 0xFFFFu) * to_f32<E>(o[w] & 0xFFFFu);
+        part += to_f32<E>(dof[t][w] >> 16) * to_f32<E>(o[w] >> 16);
+      }
+    }
+    delta = halfwave_sum(part);
+  }
+  const float lse = Lse[(size_t)bh * S + m];
+
+  TileOffsets<ROWB> to;
+  to.init(lane);
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+
+  // DMA of the K and V tiles of key tile j (row-major, swizzled) into an LDS buffer.
+  const int drow = lane / CPR, dch = lane % CPR;
+  auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+    const size_t off = (size_t)j * TILE;
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      const unsigned char* g = (part == 0 ? Kb : Vb) + off;
+#pragma unroll
+      for (int x = 0; x < (NBLK + NW - 1) / NW; ++x) {
+        const int blk = wave + x * NW;
+        if (NBLK % NW == 0 || blk < NBLK) {
+          const int row = blk * (1024 / ROWB) + drow;
+          __builtin_amdgcn_global_load_lds(g + row * ROWB + ((dch ^ bswz(row, CPR)) << 4),
+                                           (__attribute__((address_space(3))) void*)(buf + part * TILE + blk * 1024),
+                                           16, 0, 0);
+        }
+      }
+    }
+  };
+
+  auto compute = [&](const unsigned char* Ks, int k0, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(mask_tag)::value;
+    const unsigned char* Vs = Ks + TILE;
+    int nvalid = NB;
+    if constexpr (MASKED) {
+      nvalid = (q0 + 32 - k0) / 32;
+      nvalid = nvalid > NB ? NB : nvalid;
+      if (nvalid <= 0) return;
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (MASKED && nb >= nvalid) continue;
+      // S^T = K Q^T, dP^T = V dO^T: lane (c = query, hh), register g -> key 32nb + acc_row(g)
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int o = to.opnd[t & 3] + 128 * (t >> 2) + 32 * nb * ROWB;
+        s = mfma32<E>(lds_read16(Ks, o), qf[t], s);
+        dp = mfma32<E>(lds_read16(Vs, o), dof[t], dp);
+      }
+      const bool diag = MASKED && (k0 + 32 * nb == q0);
+      float ds[16];
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        float x = s[g];
+        if (diag && acc_row(g, hh) > c) x = NEG_INF;
+        const float p = fast_exp2(__builtin_fmaf(x, scale_log2, -lse));
+        ds[g] = p * (dp[g] - delta);
+      }
+      u32x4 dsk[2];
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dsk[i1][q] = pack2<E>(ds[8 * i1 + 2 * q], ds[8 * i1 + 2 * q + 1]);
+      // dQ^T += K^T dS^T (k-slots: keys 32nb + 16i1 + 8r2 + 4hh + 0..3)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const int u = 2 * nb + i1;
+          acc[db] = mfma32<E>(tr_read2(Ks, to.tr(db, u, 0), to.tr(db, u, 1)), dsk[i1], acc[db]);
+        }
+    }
+  };
+
+  auto step = [&](int j, auto par_tag, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool P = decltype(par_tag)::value;
+    unsigned char* cur = P ? lds1 : lds0;
+    unsigned char* nxt = P ? lds0 : lds1;
+    if (j + 1 < ntiles) dma_tile(j + 1, nxt);
+    compute(cur, j * BN, mask_tag);
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+  };
+
+  dma_tile(0, lds0);
+  __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+  __syncthreads();
+  int j = 0;
+  for (; j + 1 < jfull; j += 2) {
+    step(j, BTag<false>{}, BTag<false>{});
+    step(j + 1, BTag<true>{}, BTag<false>{});
+  }
+  if (j < jfull) {
+    step(j, BTag<false>{}, BTag<false>{});
+    ++j;
+  }
+  for (; j < ntiles; ++j) {
+    if (j & 1) step(j, BTag<true>{}, BTag<true>{});
+    else step(j, BTag<false>{}, BTag<true>{});
+  }
+
+  uint16_t* dqr = dQ + base + (size_t)m * D;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1)
+      gstore16(dqr + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, sm_scale));
+}
+
+// ---------------------------------------------------------------------------
+// tile_m / tile_n map to the dQ kernel's (query rows, keys per LDS tile) and the
+// dK/dV kernel's (query rows per LDS tile, keys per workgroup); at D = 128 the
+// dK/dV query tile stays at 64 rows so its double-buffered Q/dO/O tiles fit LDS.
+template <typename E, int D, int BMQ, int BNK>
+static bool launch_dkdv(const BwdArgs& a) {
+  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.H * (a.S / BNK)), dim3(2 * BNK), 0,
+                     (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
+                     (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
+                     (uint16_t*)a.dk, (uint16_t*)a.dv, a.B, a.H, a.S, a.scale_log2, a.sm_scale);
+  return hipGetLastError() == hipSuccess;
+}
+
+template <typename E, int D, int BM, int BN>
+static bool launch_dq(const BwdArgs& a) {
+  hipLaunchKernelGGL((dq_kernel<E, D, BM, BN>), dim3(a.B * a.H * (a.S / BM)), dim3(2 * BM), 0,
+                     (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
+                     (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
+                     (uint16_t*)a.dq, a.B, a.H, a.S, a.scale_log2, a.sm_scale);
+  return hipGetLastError() == hipSuccess;
+}
+
+// tile_m / tile_n map to the dQ kernel's (query rows, keys per LDS tile) and the
+// dK/dV kernel's (query rows per LDS tile, keys per workgroup); at D = 128 the
+// dK/dV query tile stays at 64 rows so its double-buffered Q/dO/O tiles fit LDS.
+template <typename E, int D, int BMQ, int BNK>
+static int launch_bwd(const BwdArgs& a) {
+  bool ok;
+  if constexpr (D == 128) ok = launch_dkdv<E, D, 64, BNK>(a);
+  else ok = launch_dkdv<E, D, BMQ, BNK>(a);
+  if (!ok) return FA_ERR_LAUNCH;
+  return launch_dq<E, D, BMQ, BNK>(a) ? FA_OK : FA_ERR_LAUNCH;
+}
+
+template <typename E, int D>
+static BwdFn pick_bwd(int bm, int bn) {
+  if (bm == 64 && bn == 64) return launch_bwd<E, D, 64, 64>;
+  if (bm == 64 && bn == 128) return launch_bwd<E, D, 64, 128>;
+  if (bm == 128 && bn == 64) return launch_bwd<E, D, 128, 64>;
+  if (bm == 128 && bn == 128) return launch_bwd<E, D, 128, 128>;
   return nullptr;
+}
+
+}  // namespace fa
+
+// FA_ETYPE (fa::F16 / fa::BF16), FA_D and FA_BWD_TABLE come from the build.
+extern "C" FA_HIDDEN fa::BwdFn FA_BWD_TABLE(int bm, int bn) {
+  return fa::pick_bwd<FA_ETYPE, FA_D>(bm, bn);
 }

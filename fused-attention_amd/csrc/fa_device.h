@@ -39,7 +39,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 struct F16 {};
 struct BF16 {};
 
-__device__ __forceinline__ int pi_swap23(int r) {
+__host__ __device__ __forceinline__ int pi_swap23(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 

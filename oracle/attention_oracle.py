@@ -41,7 +41,7 @@ def masked_scores(q, k, rows=None):
     if rows is None:
         rows = np.arange(q.shape[2])
     rows = np.asarray(rows)
-    s = np.einsum("bhrd,bhnd->bhrn", q[:, :, rows, :], k) / math.sqrt(D)
+    s = (q[:, :, rows, :] @ np.swapaxes(k, -1, -2)) / math.sqrt(D)
     future = np.arange(N)[None, :] > rows[:, None]
     s[..., future] = -np.inf
     return s

@@ -106,3 +106,10 @@ def test_error_mapping_to_reference_exceptions():
     with pytest.raises(RuntimeError):
         _lib.check(_lib.FA_ERR_LAUNCH, "x")
     _lib.check(_lib.FA_OK, "x")
+
+
+def test_no_unresolved_library_symbols():
+    """Every kernel launch stub is defined inside the library (none left for the loader)."""
+    out = os.popen(f"nm -D --undefined-only {_lib.LIB_PATH}").read()
+    missing = [line.split()[-1] for line in out.splitlines() if "_ZN2fa" in line]
+    assert not missing, missing[:5]
