@@ -117,8 +117,10 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
 
-  // work item: (b, h, key tile), heaviest key tile (j = 0) first, XCD aware
-  const int nk = S / BNK;
+  // work item: (b, h, key tile), heaviest key tile (j = 0) first, XCD aware;
+  // the last key tile may be partial (S a multiple of 64, BNK = 128): waves whose
+  // keys start past S stay inactive but still share the DMA and the barriers
+  const int nk = (S + BNK - 1) / BNK;
   const int total = B * H * nk;
   const int wg = blockIdx.x;
   const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
@@ -131,11 +133,12 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   const int k0w = jt * BNK + 32 * wave;   // first key of this wave
   const int n = k0w + c;                  // this lane's key
+  const bool active = k0w < S;            // wave-uniform; S is a multiple of 32
 
 
   // K, V rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
   u32x4 kf[KT], vf[KT];
-  {
+  if (active) {
     const uint16_t* kr = K + base + (size_t)n * D + 8 * hh;
     const uint16_t* vr = V + base + (size_t)n * D + 8 * hh;
 #pragma unroll
@@ -215,6 +218,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     for (int qb = 0; qb < QB; ++qb) {
       const int qrow0 = qtile0 + 32 * qb;   // first query of this block
       if (qrow0 + 31 < k0w) continue;       // every query precedes every key of the wave
+                                            // (always true for an inactive wave)
       // S = Q K^T and dP = dO V^T: lane (c = key, hh), register g -> query qrow0 + acc_row(g)
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -289,6 +293,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   if (i < nq) step(i, BTag<false>{});
 
   // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7
+  if (!active) return;
   uint16_t* dkr = dK + base + (size_t)n * D;
   uint16_t* dvr = dV + base + (size_t)n * D;
 #pragma unroll
@@ -472,12 +477,9 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 }
 
 // ---------------------------------------------------------------------------
-// tile_m / tile_n map to the dQ kernel's (query rows, keys per LDS tile) and the
-// dK/dV kernel's (query rows per LDS tile, keys per workgroup); at D = 128 the
-// dK/dV query tile stays at 64 rows so its double-buffered Q/dO/O tiles fit LDS.
 template <typename E, int D, int BMQ, int BNK>
 static bool launch_dkdv(const BwdArgs& a) {
-  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.H * (a.S / BNK)), dim3(2 * BNK), 0,
+  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.H * ((a.S + BNK - 1) / BNK)), dim3(2 * BNK), 0,
                      (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
                      (uint16_t*)a.dk, (uint16_t*)a.dv, a.B, a.H, a.S, a.scale_log2, a.sm_scale);
@@ -493,15 +495,14 @@ static bool launch_dq(const BwdArgs& a) {
   return hipGetLastError() == hipSuccess;
 }
 
-// tile_m / tile_n map to the dQ kernel's (query rows, keys per LDS tile) and the
-// dK/dV kernel's (query rows per LDS tile, keys per workgroup); at D = 128 the
-// dK/dV query tile stays at 64 rows so its double-buffered Q/dO/O tiles fit LDS.
+// tile_m / tile_n set the dQ kernel's query rows per workgroup and keys per LDS
+// tile.  The dK/dV kernel always runs 4 waves (128 keys) per workgroup over
+// 64-row query tiles: with its K/V rows and two accumulators in registers it
+// holds one wave per SIMD at D = 128, and this shape keeps every SIMD busy and
+// the double-buffered Q/dO/O tiles inside LDS for every head dim.
 template <typename E, int D, int BMQ, int BNK>
 static int launch_bwd(const BwdArgs& a) {
-  bool ok;
-  if constexpr (D == 128) ok = launch_dkdv<E, D, 64, BNK>(a);
-  else ok = launch_dkdv<E, D, BMQ, BNK>(a);
-  if (!ok) return FA_ERR_LAUNCH;
+  if (!launch_dkdv<E, D, 64, 128>(a)) return FA_ERR_LAUNCH;
   return launch_dq<E, D, BMQ, BNK>(a) ? FA_OK : FA_ERR_LAUNCH;
 }
 

@@ -152,3 +152,11 @@ def test_backward_rejects_gqa_and_fp32():
         fused_attention_autograd(q, q[:, :2].contiguous(), q[:, :2].contiguous())
     with pytest.raises(TypeError):
         fused_attention_autograd(q.float(), q.float(), q.float())
+
+
+@pytest.mark.parametrize("N", [64, 192, 320])
+@pytest.mark.parametrize("D", [64, 128])
+def test_backward_partial_key_tile(N, D):
+    """S not a multiple of the dK/dV kernel's 128-key workgroup: its upper waves idle."""
+    q, k, v, do = inputs((1, 2, N, D), seed=N + D, dtype=torch.bfloat16)
+    check_grads(q, k, v, do, (64, 64), f"bwd partial N{N} D{D}")
