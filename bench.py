@@ -47,6 +47,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-bwd", action="store_true", help="skip the forward+backward timing")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline wall time")
+    p.add_argument("--traffic-run", action="store_true",
+                   help="only run one 1 GiB device copy and --steps forward launches (for rocprofv3 "
+                        "--pmc FETCH_SIZE / WRITE_SIZE: the copy calibrates the counters)")
     return p.parse_args()
 
 
@@ -140,6 +143,19 @@ def main():
     q, k, v, do = (torch.randn(B, H, S, D, device="cuda", generator=g, dtype=torch.float32).bfloat16()
                    for _ in range(4))
     flops = causal_fwd_flops(B, H, S, D)
+
+    if args.traffic_run:
+        src = torch.empty(1 << 29, device="cuda", dtype=torch.int16).fill_(1)  # 1 GiB
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # calibration: reads 1 GiB, writes 1 GiB
+        torch.cuda.synchronize()
+        del src, dst
+        for _ in range(args.steps):
+            fused_attention(q, k, v, tm, tn)
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_run": True, "copy_bytes": 1 << 30, "fwd_launches": args.steps}), flush=True)
+        return
 
     fused_attention(q, k, v, tm, tn)  # first call
     torch.cuda.synchronize()
