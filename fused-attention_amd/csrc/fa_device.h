@@ -74,6 +74,22 @@ __device__ __forceinline__ uint32_t pack2<F16>(float x, float y) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// acc + (sum of the two 16-bit values packed in w): v_dot2c_f32_{bf16,f16}
+// against the pair (1, 1), i.e. one instruction for two adds.
+template <typename E>
+__device__ __forceinline__ float add_pair(uint32_t w, float acc);
+
+template <>
+__device__ __forceinline__ float add_pair<BF16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                         acc, false);
+}
+
+template <>
+__device__ __forceinline__ float add_pair<F16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
+}
+
 // One 16-bit element -> fp32.
 template <typename E>
 __device__ __forceinline__ float to_f32(uint32_t bits16);
@@ -124,6 +140,21 @@ __device__ __forceinline__ void lds_write16(unsigned char* base, int byte_off, c
 
 __device__ __forceinline__ void lds_write8(unsigned char* base, int byte_off, const u32x2& v) {
   *reinterpret_cast<u32x2*>(base + byte_off) = v;
+}
+
+// Buffer descriptor for raw byte-addressed loads from [p, p + bytes): word 3 =
+// 0x00020000 is the gfx9 setting for untyped dword access; loads past `bytes`
+// (vector offset) read zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+// Global -> LDS DMA of 16 bytes per lane (buffer_load_dwordx4 ... lds): lane L
+// reads rsrc bytes [voff + soff, +16) and writes them to lds + 16 L.
+// (Kept out of kernel bodies: clang's host pass drops a kernel's launch stub
+// when these builtins appear inside the kernel's own lambdas.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, unsigned char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
 __device__ __forceinline__ u32x4 gload16(const uint16_t* p) {

@@ -8,15 +8,18 @@
 //     s = -inf where key > query    (only on tiles that straddle the diagonal)
 //     m_new = max(m, rowmax(s) * c) with c = log2(e)/sqrt(D)
 //     alpha = exp2(m - m_new); p = exp2(s*c - m_new)
-//     l = l*alpha + rowsum(p)       (unrounded p)
-//     acc = acc*alpha + p(rounded to the input type) . v
+//     P = p rounded to the input type
+//     l = l*alpha + rowsum(P)
+//     acc = acc*alpha + P . v
 //   O = acc / l; optional LSE = m + log2(l) (fused_backward.py:169).
-// The rescale of acc and l is skipped for a tile when no row of the wave has a
-// new maximum (alpha would be exactly 1).  FA_RESCALE_THRESHOLD > 0 widens the
-// skip to max increases below that many powers of two (p then stays <= 2^T);
-// O = acc / l and LSE = m + log2(l) do not depend on the reference point, but
-// a dominant p is then no longer exactly 1 before its rounding to 16 bits, so
-// the default threshold is 0.
+// Two differences from the reference's arithmetic, both far inside the fp32
+// reference's tolerance: l sums the rounded P that the PV product uses (the
+// reference sums the unrounded p, fused.py:59), so O is an exactly normalised
+// average of the V rows it weights; and the running max is lazy: acc and l are
+// rescaled only when some row's max grows by more than FA_RESCALE_THRESHOLD
+// powers of two (p then stays <= 2^T).  O = acc / l and LSE = m + log2(l) do
+// not depend on the reference point m, and because l sums the same rounded
+// weights as acc, a row dominated by one key still reproduces that key's V row.
 //
 // MI355X mapping:
 //   * one workgroup = GH query heads (sharing one K/V head) x BM query rows;
@@ -25,7 +28,8 @@
 //     row: row max / row sum are register-local plus one permlane32 swap, and the
 //     score accumulator is fed straight back as the B operand of O^T += V^T P^T.
 //   * Q stays in registers for the whole loop.  K and V tiles go global -> LDS
-//     with global_load_lds_dwordx4 (no VGPR staging), double-buffered in two
+//     with buffer_load_dwordx4 ... lds (no VGPR staging; the per-lane source
+//     offsets are fixed, the tile offset is a scalar), double-buffered in two
 //     LDS arrays; the next tile's DMA runs while the current tile is computed.
 //   * V^T operands come from ds_read_b64_tr_b16 on the row-major V tile, so no
 //     transpose is ever materialised.
@@ -36,10 +40,15 @@
 //     (batch, head-group) units; inside a unit the last (heaviest) query tile
 //     is dispatched first.
 //
-// LDS layouts (one buffer = K tile then V tile, each BN rows x D, row-major):
-//   K: 16-byte chunk ch of row r stored at chunk ch ^ (r & 7); an MFMA A-operand
-//      read (lane c reads row c, one chunk) then hits 8 distinct bank groups per
-//      8 lanes.
+// LDS layouts (one buffer = K tile then V tile, each BN rows x D, row-major).
+// gfx950's LDS has 64 banks of 4 bytes: a 16-byte read is served 16 lanes per
+// cycle and an 8-byte read 16 lanes per cycle (measured: 16-byte reads stream at
+// twice the bytes per clock of 8-byte reads), so a read is conflict free when
+// the lanes of each 16-lane phase touch distinct banks.
+//   K: 16-byte chunk ch of row r stored at chunk ch ^ kswz(r), kswz(r) =
+//      (r * CPR / 16) & (CPR - 1) with CPR chunks per row; an MFMA A-operand
+//      read (lane c reads row c, one chunk) then puts the 16 lanes of a phase
+//      on 16 distinct 16-byte bank slots.
 //   V: byte b of row r stored at b ^ (32 * (r & 3)); a transposed read (16 lanes
 //      = 4 rows x 32 bytes) then hits 4 distinct 32-byte bank groups.
 #include "fa_device.h"
@@ -54,7 +63,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 constexpr int kWaitVmcnt0 = 0x0F70;
 // skip the rescale unless a row max grows by more than this (log2 units)
 #ifndef FA_RESCALE_THRESHOLD
-#define FA_RESCALE_THRESHOLD 0.0f
+#define FA_RESCALE_THRESHOLD 8.0f
 #endif
 constexpr float kRescaleThreshold = FA_RESCALE_THRESHOLD;
 
@@ -91,7 +100,7 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   constexpr int TILE = BN * ROWB;      // bytes per K or V tile
   constexpr int NBLK = TILE / 1024;    // 1 KB DMA blocks per tile
   constexpr int CPR = ROWB / 16;       // 16-byte chunks per row
-  constexpr int KMASK = (CPR >= 8 ? 8 : CPR) - 1;
+  constexpr int NDMA = (NBLK + NW - 1) / NW;  // DMA blocks per wave per tile (K and V each)
   static_assert(TILE % 1024 == 0, "tile must be whole 1 KB DMA blocks");
   const float NEG_INF = -__builtin_inff();
 
@@ -129,23 +138,26 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   // ---- DMA of one K/V tile into an LDS buffer: 1 KB per wave instruction,
   // lane L's 16 bytes land at block + 16 L; the lane loads the global bytes
-  // that belong there under the swizzles above.
+  // that belong there under the swizzles above.  A lane's source offsets inside
+  // a tile are fixed (kvo / vvo); the tile offset j*TILE is a scalar (soffset).
   const int drow = lane / CPR;                 // row inside a 1 KB block
   const int dpos = (lane % CPR) * 16;          // LDS byte offset inside the row
-  auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
-    const unsigned char* Kt = Kbh + (size_t)j * TILE;
-    const unsigned char* Vt = Vbh + (size_t)j * TILE;
+  int kvo[NDMA], vvo[NDMA];
 #pragma unroll
-    for (int i = 0; i < (NBLK + NW - 1) / NW; ++i) {
+  for (int i = 0; i < NDMA; ++i) {
+    const int row = (wave + i * NW) * (1024 / ROWB) + drow;
+    kvo[i] = row * ROWB + (((dpos >> 4) ^ ((row * CPR / 16) & (CPR - 1))) << 4);
+    vvo[i] = row * ROWB + (dpos ^ ((32 * (row & 3)) & (ROWB - 1)));
+  }
+  const auto krs = make_rsrc(Kbh, S * ROWB);
+  const auto vrs = make_rsrc(Vbh, S * ROWB);
+  auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
       const int blk = wave + i * NW;
       if (NBLK % NW == 0 || blk < NBLK) {
-        const int row = blk * (1024 / ROWB) + drow;
-        const int kpos = (((dpos >> 4) ^ (row & KMASK)) << 4);
-        const int vpos = dpos ^ ((32 * (row & 3)) & (ROWB - 1));
-        __builtin_amdgcn_global_load_lds(Kt + row * ROWB + kpos,
-                                         (__attribute__((address_space(3))) void*)(buf + blk * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(Vt + row * ROWB + vpos,
-                                         (__attribute__((address_space(3))) void*)(buf + TILE + blk * 1024), 16, 0, 0);
+        dma16(krs, buf + blk * 1024, kvo[i], j * TILE);
+        dma16(vrs, buf + TILE + blk * 1024, vvo[i], j * TILE);
       }
     }
   };
@@ -160,10 +172,10 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   dma_tile(0, lds0);
 
   // ---- per-lane LDS operand offsets
-  // K A-operand, k-step t: row c, chunk (2t+hh) ^ (c & KMASK) -> koff[t&3] + 128*(t>>2)
-  int koff[4];
+  // K A-operand, k-step t: row c (+ 32 nb), chunk (2t+hh) ^ kswz(c)
+  int koff[KT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) koff[t] = c * ROWB + ((((2 * t + hh) & (CPR - 1)) ^ (c & KMASK)) << 4);
+  for (int t = 0; t < KT; ++t) koff[t] = c * ROWB + (((2 * t + hh) ^ ((c * CPR / 16) & (CPR - 1))) << 4);
   // V^T A-operand via transposed reads: in 16-lane group G, lane (kr, c4) addresses
   // key row 4hh + kr (+ block offsets) and the 4 columns feeding output lanes
   // 4c4..4c4+3, which hold d = pi(16(G&1) + 4c4) + 0..3 of the 32-d block.
@@ -202,7 +214,7 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
         f32x16 x = f32x16{};
 #pragma unroll
         for (int t = 0; t < KT; ++t)
-          x = mfma32<E>(lds_read16(Ks, koff[t & 3] + 128 * (t >> 2) + nb * 32 * ROWB), qf[t], x);
+          x = mfma32<E>(lds_read16(Ks, koff[t] + nb * 32 * ROWB), qf[t], x);
         s[nb] = x;
       }
     }
@@ -238,27 +250,28 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
     // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
     // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7)
+    // l sums the rounded P two at a time (v_dot2c with (1, 1)).
     u32x4 pk[2 * NB];
-    float lsum = 0.f;
+    float lsum[2] = {0.f, 0.f};
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if (!MASKED || nb < nvalid) {
         float p[16];
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
-          p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
-          lsum += p[g];
-        }
+        for (int g = 0; g < 16; ++g) p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
 #pragma unroll
         for (int i1 = 0; i1 < 2; ++i1) {
           u32x4 w;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+          for (int q = 0; q < 4; ++q) {
+            w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+            lsum[i1] = add_pair<E>(w[q], lsum[i1]);
+          }
           pk[2 * nb + i1] = w;
         }
       }
     }
-    lrun += lsum;
+    lrun += lsum[0] + lsum[1];
 
     // O^T += V^T P^T; operand rows are d = 32db + pi(row), keys per slot as above
 #pragma unroll
