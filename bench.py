@@ -1,11 +1,12 @@
 """Throughput of the fused causal attention path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--tile-m 128 --tile-n 64] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--device-warmup-s T] [--tile-m 128 --tile-n 64] [--no-cpu-baseline]
 
 One step = one fused causal forward over the full workload B=4, H=32, S=4096,
 D=128 in bfloat16 (inputs resident in HBM).  K steps are timed between two
-device synchronisations; the forward+backward of the same shape (through the
-autograd Function) is timed the same way when the backward kernels exist.
+device synchronisations, after T seconds (default 1.5) of untimed steps that let
+the GPU clocks settle and W untimed warm-up steps; the forward+backward of the
+same shape (through the autograd Function) is timed the same way.
 FLOPs follow the reference's causal convention: 2*B*H*S^2*D for the forward,
 2.5x that for the backward (benchmarks/benchmark_forward.py:206,
 benchmarks/benchmark_backward.py:126-127).
@@ -47,6 +48,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-bwd", action="store_true", help="skip the forward+backward timing")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline wall time")
+    p.add_argument("--device-warmup-s", type=float, default=1.5,
+                   help="untimed seconds of the step before the warm-up steps (GPU clock ramp)")
     p.add_argument("--traffic-run", action="store_true",
                    help="only run one 1 GiB device copy and --steps forward launches (for rocprofv3 "
                         "--pmc FETCH_SIZE / WRITE_SIZE: the copy calibrates the counters)")
@@ -67,8 +70,22 @@ def traffic_from_profile():
     return float(m.group(1)) if m else None
 
 
-def time_steps(fn, steps, warmup, torch):
+def device_warmup(fn, seconds, torch):
+    """Run the step untimed until `seconds` have passed, so the GPU clocks have
+    settled before the warm-up steps (a cold MI355X ramps for about a second)."""
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
+def time_steps(fn, steps, warmup, torch, warm_seconds):
     """Per-step event timing on the current (launch) stream, plus wall time of the whole run."""
+    device_warmup(fn, warm_seconds, torch)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -160,7 +177,7 @@ def main():
     fused_attention(q, k, v, tm, tn)  # first call
     torch.cuda.synchronize()
     ms_step, kern_ms_mean, kern_ms_med = time_steps(lambda: fused_attention(q, k, v, tm, tn),
-                                                   args.steps, args.warmup, torch)
+                                                   args.steps, args.warmup, torch, args.device_warmup_s)
     fwd_tflops = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (kern_ms_mean * 1e-3) / 1e12
 
@@ -179,7 +196,8 @@ def main():
         "data": "synthetic: Q, K, V, dO ~ N(0,1) from torch.Generator(cuda).manual_seed(0), cast to bf16",
         "config": {"workload": "causal MHA forward B=4 H=32 S=4096 D=128 bf16", "B": B, "H": H, "S": S,
                    "D": D, "tile_m": tm, "tile_n": tn, "flops_per_step": flops,
-                   "flop_convention": "causal 2*B*H*S^2*D (fwd), 3.5x for fwd+bwd"},
+                   "flop_convention": "causal 2*B*H*S^2*D (fwd), 3.5x for fwd+bwd",
+                   "device_warmup_s": args.device_warmup_s},
         "pct_of_peak": round(100.0 * fwd_tflops / PEAK_BF16_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
@@ -198,7 +216,7 @@ def main():
 
         step()
         torch.cuda.synchronize()
-        fb_ms, _, fb_med = time_steps(step, args.steps, args.warmup, torch)
+        fb_ms, _, fb_med = time_steps(step, args.steps, args.warmup, torch, args.device_warmup_s)
         fb_tflops = 3.5 * flops / (fb_ms * 1e-3) / 1e12
         result["fwd_bwd"] = {"value": round(fb_tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(fb_ms, 4),
                              "pct_of_peak": round(100.0 * fb_tflops / PEAK_BF16_TFLOPS, 2),

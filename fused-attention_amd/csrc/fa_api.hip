@@ -40,9 +40,11 @@ fa::BwdFn bwd_table(int dtype, int D, int bm, int bn) {
 }
 
 // Query heads per workgroup for a GQA group: as many heads of one K/V group
-// as fit in 8 waves (512 threads), each head taking block_m/32 waves.
-int heads_per_wg(int group, int block_m) {
-  int cap = 256 / block_m;  // 8 waves / (block_m / 32)
+// as fit in 8 waves (512 threads), each head taking block_m/32 waves.  With
+// 128-key tiles a wave holds two 128-key score tiles in flight and needs more
+// than the 256 VGPRs of two waves per SIMD, so the workgroup stays at 4 waves.
+int heads_per_wg(int group, int block_m, int block_n) {
+  int cap = (block_n == 128 ? 128 : 256) / block_m;  // waves / (block_m / 32)
   if (cap > kMaxGroupHeadsPerWg) cap = kMaxGroupHeadsPerWg;
   int gh = 1;
   while (gh * 2 <= cap && group % (gh * 2) == 0) gh *= 2;
@@ -73,7 +75,7 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   if (st != FA_OK) return st;
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o) return FA_ERR_NULL;
-  const int gh = heads_per_wg(H / H_kv, block_m);
+  const int gh = heads_per_wg(H / H_kv, block_m, block_n);
   fa::FwdFn fn = fwd_table(dtype, D, block_m, block_n, gh, lse != nullptr);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::FwdArgs a{q, k, v, o, lse, B, H, H_kv, S, D, scale_log2, hip_stream};
@@ -97,7 +99,7 @@ int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with
   if (check_common(1, 1, 256, D, dtype, block_m, block_n) != FA_OK) return 0;
   if (group <= 0) return 0;
   if (is_bwd) return (group == 1 && bwd_table(dtype, D, block_m, block_n)) ? 1 : 0;
-  return fwd_table(dtype, D, block_m, block_n, heads_per_wg(group, block_m), with_lse) ? 1 : 0;
+  return fwd_table(dtype, D, block_m, block_n, heads_per_wg(group, block_m, block_n), with_lse) ? 1 : 0;
 }
 
 const char* fa_strerror(int status) {

@@ -15,11 +15,14 @@
 // Two differences from the reference's arithmetic, both far inside the fp32
 // reference's tolerance: l sums the rounded P that the PV product uses (the
 // reference sums the unrounded p, fused.py:59), so O is an exactly normalised
-// average of the V rows it weights; and the running max is lazy: acc and l are
-// rescaled only when some row's max grows by more than FA_RESCALE_THRESHOLD
-// powers of two (p then stays <= 2^T).  O = acc / l and LSE = m + log2(l) do
-// not depend on the reference point m, and because l sums the same rounded
-// weights as acc, a row dominated by one key still reproduces that key's V row.
+// average of the V rows it weights; and the reference point m is lazy: a tile's
+// p is computed against the current m, and only if some lane's sum of p over
+// the tile exceeds 2^FA_RESCALE_THRESHOLD (or is not finite) is the tile's row
+// max taken, acc and l rescaled and p recomputed.  Every p therefore stays
+// <= 2^T, no row max is reduced on the common path, and O = acc / l and
+// LSE = m + log2(l) do not depend on the reference point; because l sums the
+// same rounded weights as acc, a row dominated by one key still reproduces
+// that key's V row exactly.
 //
 // MI355X mapping:
 //   * one workgroup = GH query heads (sharing one K/V head) x BM query rows;
@@ -61,20 +64,27 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 constexpr int kWaitVmcnt0 = 0x0F70;
-// skip the rescale unless a row max grows by more than this (log2 units)
+// p is recomputed against a fresh row max only when a lane's sum of p over a
+// tile exceeds 2^FA_RESCALE_THRESHOLD
 #ifndef FA_RESCALE_THRESHOLD
-#define FA_RESCALE_THRESHOLD 8.0f
+#define FA_RESCALE_THRESHOLD 8
 #endif
-constexpr float kRescaleThreshold = FA_RESCALE_THRESHOLD;
+constexpr float kSumLimit = float(1 << FA_RESCALE_THRESHOLD);
 
 template <int D, int BM, int BN, int GH>
 constexpr int fwd_waves_per_simd() {
   return (BN == 64 && (BM / 32) * GH >= 4) ? 2 : 1;
 }
 
+// Compile-time "tile is below the diagonal" marker, and its run-time twin.
 template <bool B>
 struct Tag {
   static constexpr bool value = B;
+  static constexpr bool is_dynamic = false;
+};
+struct Dyn {
+  bool value;
+  static constexpr bool is_dynamic = true;
 };
 
 // Two 8-byte transposed LDS reads -> one 16-byte MFMA operand.
@@ -104,8 +114,8 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   static_assert(TILE % 1024 == 0, "tile must be whole 1 KB DMA blocks");
   const float NEG_INF = -__builtin_inff();
 
-  __shared__ __attribute__((aligned(1024))) unsigned char lds0[2 * TILE];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds1[2 * TILE];
+  // K buffers at [0, 2 TILE), V buffers at [2 TILE, 4 TILE)
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -151,14 +161,18 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   }
   const auto krs = make_rsrc(Kbh, S * ROWB);
   const auto vrs = make_rsrc(Vbh, S * ROWB);
-  auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+  auto dma_k = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int blk = wave + i * NW;
-      if (NBLK % NW == 0 || blk < NBLK) {
-        dma16(krs, buf + blk * 1024, kvo[i], j * TILE);
-        dma16(vrs, buf + TILE + blk * 1024, vvo[i], j * TILE);
-      }
+      if (NBLK % NW == 0 || blk < NBLK) dma16(krs, buf + blk * 1024, kvo[i], j * TILE);
+    }
+  };
+  auto dma_v = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int blk = wave + i * NW;
+      if (NBLK % NW == 0 || blk < NBLK) dma16(vrs, buf + blk * 1024, vvo[i], j * TILE);
     }
   };
 
@@ -169,7 +183,6 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 #pragma unroll
     for (int t = 0; t < KT; ++t) qf[t] = gload16(qrow + 16 * t);
   }
-  dma_tile(0, lds0);
 
   // ---- per-lane LDS operand offsets
   // K A-operand, k-step t: row c (+ 32 nb), chunk (2t+hh) ^ kswz(c)
@@ -194,68 +207,70 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
   float mrun = NEG_INF, lrun = 0.f;
 
-  // ---- one key tile
-  auto compute = [&](const unsigned char* Ks, int k0, auto mask_tag) __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(mask_tag)::value;
-    const unsigned char* Vs = Ks + TILE;
-    int nvalid = NB;
-    if constexpr (MASKED) {
-      nvalid = (q0 + 32 - k0) / 32;
-      nvalid = nvalid > NB ? NB : nvalid;
-      if (nvalid <= 0) return;
-    }
+  // ---- pipeline stages.  `mt` is Tag<false> for tiles wholly below the
+  // diagonal (everything compile-time) or Dyn for the generic path, where
+  // `mt.value` says whether the tile straddles the diagonal (wave-uniform).
+  // Valid 32-key blocks of a tile for this wave (<= 0: none).
+  auto valid_blocks = [&](int k0, auto mt) __attribute__((always_inline)) {
+    if (!mt.value) return NB;
+    const int n = (q0 + 32 - k0) / 32;
+    return n > NB ? NB : n;
+  };
 
-    // S^T = K Q^T: A row c <- key 32nb + c; register g of lane (c, hh) holds
-    // key offset 8*(g/4) + 4*hh + (g%4) of the block, query c
-    f32x16 s[NB];
+  // S^T = K Q^T: A row c <- key 32nb + c; register g of lane (c, hh) holds
+  // key offset 8*(g/4) + 4*hh + (g%4) of the block, query c.  Keys past the
+  // query are set to -inf on the diagonal block.
+  auto s_tile = [&](const unsigned char* Ks, int k0, int nv, auto mt, f32x16 (&s)[NB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      if (!MASKED || nb < nvalid) {
+      if (!mt.value || nb < nv) {
         f32x16 x = f32x16{};
 #pragma unroll
-        for (int t = 0; t < KT; ++t)
-          x = mfma32<E>(lds_read16(Ks, koff[t] + nb * 32 * ROWB), qf[t], x);
-        s[nb] = x;
-      }
-    }
-
-    float mx = NEG_INF;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (!MASKED || nb < nvalid) {
-        if (MASKED && k0 + 32 * nb == q0) {
+        for (int t = 0; t < KT; ++t) x = mfma32<E>(lds_read16(Ks, koff[t] + nb * 32 * ROWB), qf[t], x);
+        if (mt.value && k0 + 32 * nb == q0) {
 #pragma unroll
           for (int g = 0; g < 16; ++g) {
             const int koffs = 8 * (g >> 2) + 4 * hh + (g & 3);
-            if (koffs > c) s[nb][g] = NEG_INF;
+            if (koffs > c) x[g] = NEG_INF;
           }
         }
+        s[nb] = x;
+      }
+    }
+  };
+
+  // Row max of a tile in scaled log2 units (-inf where the wave has no valid block).
+  auto tile_max = [&](const f32x16 (&s)[NB], int nv, auto mt) __attribute__((always_inline)) {
+    float mx = NEG_INF;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      if (!mt.value || nb < nv) {
 #pragma unroll
         for (int g = 0; g < 16; ++g) mx = fmaxf(mx, s[nb][g]);
       }
-    }
-    mx = halfwave_max(mx) * scale_log2;
+    return halfwave_max(mx) * scale_log2;
+  };
 
-    // move the reference max (and rescale) only when some row's max grows
-    if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleThreshold)) {
-      const float mnew = fmaxf(mrun, mx);
-      const float alpha = fast_exp2(mrun - mnew);
-      mrun = mnew;
-      lrun *= alpha;
+  // Move the reference point to mx (or keep it if larger): rescale acc and l.
+  auto rescale_to = [&](float mx) __attribute__((always_inline)) {
+    const float mnew = fmaxf(mrun, mx);
+    const float alpha = fast_exp2(mrun - mnew);
+    mrun = mnew;
+    lrun *= alpha;
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int g = 0; g < 16; ++g) acc[db][g] *= alpha;
-    }
+      for (int g = 0; g < 16; ++g) acc[db][g] *= alpha;
+  };
 
-    // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
-    // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7)
-    // l sums the rounded P two at a time (v_dot2c with (1, 1)).
-    u32x4 pk[2 * NB];
+  // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
+  // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7);
+  // returns this lane's sum of the rounded P (v_dot2c with (1, 1)).
+  auto exp_tile = [&](const f32x16 (&s)[NB], int nv, auto mt, u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
     float lsum[2] = {0.f, 0.f};
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      if (!MASKED || nb < nvalid) {
+      if (!mt.value || nb < nv) {
         float p[16];
 #pragma unroll
         for (int g = 0; g < 16; ++g) p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
@@ -271,15 +286,28 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
         }
       }
     }
-    lrun += lsum[0] + lsum[1];
+    return lsum[0] + lsum[1];
+  };
 
-    // O^T += V^T P^T; operand rows are d = 32db + pi(row), keys per slot as above
+  // P of a tile against the lazy reference point, and the l update.  The
+  // first tile always takes the slow path (m = -inf gives p = inf).
+  auto softmax = [&](const f32x16 (&s)[NB], int nv, auto mt, u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
+    float ts = exp_tile(s, nv, mt, pk);
+    if (__builtin_amdgcn_ballot_w64(!(ts <= kSumLimit))) {
+      rescale_to(tile_max(s, nv, mt));
+      ts = exp_tile(s, nv, mt, pk);
+    }
+    lrun += ts;
+  };
+
+  // O^T += V^T P^T; operand rows are d = 32db + pi(row), keys per slot as above.
+  auto pv = [&](const unsigned char* Vs, const u32x4 (&pk)[2 * NB], int nv, auto mt) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const int vb = ((db & 1) ? voff_odd : voff_even) + 64 * db;
 #pragma unroll
       for (int u = 0; u < 2 * NB; ++u) {
-        if (!MASKED || (u >> 1) < nvalid) {
+        if (!mt.value || (u >> 1) < nv) {
           const int o = vb + 16 * u * ROWB;
           acc[db] = mfma32<E>(lds_read_tr16x2(Vs, o, o + 8 * ROWB), pk[u], acc[db]);
         }
@@ -287,31 +315,61 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
   };
 
-  auto step = [&](int j, auto par_tag, auto mask_tag) __attribute__((always_inline)) {
-    constexpr bool P = decltype(par_tag)::value;
-    unsigned char* cur = P ? lds1 : lds0;
-    unsigned char* nxt = P ? lds0 : lds1;
-    if (j + 1 < ntiles) dma_tile(j + 1, nxt);
-    compute(cur, j * BN, mask_tag);
+  // ---- software pipeline over key tiles.  Iteration j: wait for K(j+1) and
+  // V(j), start the DMA of K(j+2) and V(j+1), then S(j+1) on the MFMA pipe
+  // while the VALU turns S(j) into P(j), then PV(j).  K runs one tile ahead of
+  // V; both are double-buffered.
+  auto Kbuf = [&](int j) __attribute__((always_inline)) { return lds + (j & 1) * TILE; };
+  auto Vbuf = [&](int j) __attribute__((always_inline)) { return lds + 2 * TILE + (j & 1) * TILE; };
+
+  auto iteration = [&](int j, f32x16 (&sc)[NB], int nvc, f32x16 (&sn)[NB], int& nvn, auto mt) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
+    if (j + 2 < ntiles) dma_k(j + 2, Kbuf(j));
+    if (j + 1 < ntiles) dma_v(j + 1, Vbuf(j + 1));
+    const Dyn cur{j >= jfull};
+    u32x4 pk[2 * NB];
+    if (!mt.value || j + 1 < ntiles) {
+      const Dyn nxt{j + 1 >= jfull};
+      nvn = mt.value ? valid_blocks((j + 1) * BN, nxt) : NB;
+      if constexpr (decltype(mt)::is_dynamic) {
+        s_tile(Kbuf(j + 1), (j + 1) * BN, nvn, nxt, sn);
+        softmax(sc, nvc, cur, pk);
+        pv(Vbuf(j), pk, nvc, cur);
+      } else {
+        s_tile(Kbuf(j + 1), (j + 1) * BN, NB, mt, sn);
+        softmax(sc, NB, mt, pk);
+        pv(Vbuf(j), pk, NB, mt);
+      }
+    } else {
+      softmax(sc, nvc, cur, pk);
+      pv(Vbuf(j), pk, nvc, cur);
+    }
   };
 
+  // prologue: K(0), V(0), K(1) in flight; S(0)
+  dma_k(0, Kbuf(0));
+  dma_v(0, Vbuf(0));
+  if (ntiles > 1) dma_k(1, Kbuf(1));
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
+  f32x16 sa[NB], sb[NB];
+  int nva, nvb = NB;
+  {
+    const Dyn m0{jfull == 0};
+    nva = valid_blocks(0, m0);
+    s_tile(Kbuf(0), 0, nva, m0, sa);
+  }
 
+  // tiles j with j + 1 < jfull: both S(j) and S(j+1) below the diagonal
   int j = 0;
-  for (; j + 1 < jfull; j += 2) {
-    step(j, Tag<false>{}, Tag<false>{});
-    step(j + 1, Tag<true>{}, Tag<false>{});
+  for (; j + 2 < jfull; j += 2) {
+    iteration(j, sa, NB, sb, nvb, Tag<false>{});
+    iteration(j + 1, sb, NB, sa, nva, Tag<false>{});
   }
-  if (j < jfull) {
-    step(j, Tag<false>{}, Tag<false>{});
-    ++j;
-  }
-  for (; j < ntiles; ++j) {
-    if (j & 1) step(j, Tag<true>{}, Tag<true>{});
-    else step(j, Tag<false>{}, Tag<true>{});
+  for (; j < ntiles; j += 2) {
+    iteration(j, sa, nva, sb, nvb, Dyn{true});
+    if (j + 1 < ntiles) iteration(j + 1, sb, nvb, sa, nva, Dyn{true});
   }
 
   // ---- epilogue: O = acc / l; lane holds d = 32db + 16i1 + 8hh + 0..7
@@ -346,8 +404,8 @@ static FwdFn pick_fwd(int bm, int bn, int gh, bool lse) {
   if (bm == BM_ && bn == BN_ && gh == GH_)                                             \
     return lse ? launch_fwd<E, D, BM_, BN_, GH_, true> : launch_fwd<E, D, BM_, BN_, GH_, false>;
   FA_CASE(64, 64, 1) FA_CASE(64, 128, 1) FA_CASE(128, 64, 1) FA_CASE(128, 128, 1)
-  FA_CASE(64, 64, 2) FA_CASE(64, 128, 2) FA_CASE(128, 64, 2) FA_CASE(128, 128, 2)
-  FA_CASE(64, 64, 4) FA_CASE(64, 128, 4)
+  FA_CASE(64, 64, 2) FA_CASE(64, 128, 2) FA_CASE(128, 64, 2)
+  FA_CASE(64, 64, 4)
 #undef FA_CASE
   return nullptr;
 }
