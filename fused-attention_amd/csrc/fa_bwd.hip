@@ -21,10 +21,12 @@
 //                accumulates dQ^T += K^T dS^T, reading K^T with transposed reads.
 // Neither kernel uses atomics or a workspace; each output element is written once.
 //
-// LDS tiles are row-major with 16-byte chunk ch of row r stored at
-// ch ^ bswz(r), bswz(r) = 2*(r & 3) + ((r >> 2) & 1): 8 consecutive rows read at
-// one chunk hit 8 distinct bank groups (MFMA operand reads), and 4 consecutive
-// rows read as 32-byte pieces (transposed reads) hit 4 distinct 32-byte groups.
+// LDS tiles are row-major with 16-byte chunk ch of row r stored at ch ^ bswz(r).
+// gfx950's LDS has 64 banks of 4 bytes and serves a 16-byte read 16 lanes per
+// cycle, an 8-byte read 16 lanes per cycle.  bswz makes both read kinds conflict
+// free: 16 consecutive rows read at one chunk (an MFMA operand read) land on 16
+// distinct 16-byte slots of the 256-byte bank line, and 4 consecutive rows read
+// as one 32-byte piece (a transposed read) land on 4 distinct 32-byte groups.
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -40,11 +42,15 @@ struct BTag {
   static constexpr bool value = B;
 };
 
-// Chunk swizzle of row r for rows of cpr 16-byte chunks.  A plain function (not a
-// template): a template call inside the LDS-DMA builtin's operands keeps clang
-// from emitting the kernel's host-side launch stub.
+// Chunk swizzle of row r for rows of cpr 16-byte chunks (cpr = 16, 8 or 4: rows
+// of 256, 128 or 64 bytes, i.e. 1, 2 or 4 rows per bank line).
 __host__ __device__ __forceinline__ int bswz(int r, int cpr) {
-  return ((((r & 3) << 1) | ((r >> 2) & 1))) & ((cpr >= 8 ? 8 : cpr) - 1);
+  if (cpr >= 16) return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8);
+  if (cpr == 8) {
+    const int k = r >> 1;
+    return ((k & 3) << 1) | ((k >> 2) & 1);
+  }
+  return (r >> 2) & 3;
 }
 
 __device__ __forceinline__ u32x4 tr_read2(const unsigned char* base, int off0, int off1) {
@@ -55,32 +61,32 @@ __device__ __forceinline__ u32x4 tr_read2(const unsigned char* base, int off0, i
 }
 
 // Per-lane offsets into a swizzled row-major tile with rows of ROWB bytes.
-//  opnd[t&3] + 128*(t>>2): MFMA operand read, lane c -> row c, chunk 2t + hh
-//  tr_even / tr_odd + 64*db + (16u + 8r2)*ROWB: transposed read feeding an A
-//    operand whose rows are d = 32db + pi(lane % 32) and whose k-slots are rows
-//    16u + 8*r2 + 4*hh + (0..3) of the tile (the slot order of a score
-//    accumulator used as the B operand)
+//  opnd[t] (+ 32 qb * ROWB): MFMA operand read, lane c -> row c, chunk 2t + hh
+//  tr(db, u, r2): transposed read feeding an A operand whose rows are
+//    d = 32db + pi(lane % 32) and whose k-slots are rows 16u + 8*r2 + 4*hh + (0..3)
+//    of the tile (the slot order of a score accumulator used as the B operand);
+//    the swizzle of those rows depends only on (r2, hh, lane), not on u.
 template <int ROWB>
 struct TileOffsets {
-  int opnd[4];
-  int tr_even, tr_odd;
+  static constexpr int CPR = ROWB / 16, KT = ROWB / 32, DB = ROWB / 64;
+  int opnd[KT];
+  int trv[DB][2];
   __device__ __forceinline__ void init(int lane) {
-    constexpr int CPR = ROWB / 16;
     const int c = lane & 31, hh = lane >> 5;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) opnd[t] = c * ROWB + ((((2 * t + hh) & (CPR - 1)) ^ bswz(c, CPR)) << 4);
+    for (int t = 0; t < KT; ++t) opnd[t] = c * ROWB + (((2 * t + hh) ^ bswz(c, CPR)) << 4);
     const int G = lane >> 4, kr = (lane >> 2) & 3, c4 = lane & 3;
-    const int x = (2 * pi_swap23(16 * (G & 1) + 4 * c4)) >> 4;  // chunk 0..3 of the 64-byte d range
-    const int within = (2 * pi_swap23(16 * (G & 1) + 4 * c4)) & 8;
-    const int sl = bswz(4 * hh + kr, CPR);                        // swizzle of every row this lane reads
-    const int k1 = (CPR >= 8) ? (sl >> 2) : 0;
-    const int base = (4 * hh + kr) * ROWB + ((x ^ (sl & 3)) << 4) + within;
-    tr_even = base + 64 * k1;
-    tr_odd = base + 64 * (1 - k1) - 64;
+    const int b = 2 * pi_swap23(16 * (G & 1) + 4 * c4);   // byte offset of 4 d values in a 64-byte block
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+      const int row = 8 * r2 + 4 * hh + kr;
+      const int w = bswz(row, CPR);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        trv[db][r2] = row * ROWB + ((((64 * db + b) >> 4) ^ w) << 4) + (b & 8);
+    }
   }
-  __device__ __forceinline__ int tr(int db, int u, int r2) const {
-    return ((db & 1) ? tr_odd : tr_even) + 64 * db + (16 * u + 8 * r2) * ROWB;
-  }
+  __device__ __forceinline__ int tr(int db, int u, int r2) const { return trv[db][r2] + 16 * u * ROWB; }
 };
 
 // Score-accumulator element (lane c, hh, register g) -> row offset inside a 32-row block.
@@ -153,29 +159,33 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   // DMA of the Q, dO and O tiles (row-major, swizzled) and the LSE slice of query
   // tile i into an LDS buffer: waves take 1 KB blocks round-robin and lane L of a
-  // block writes LDS bytes blk*1024 + 16L.
+  // block writes LDS bytes blk*1024 + 16L.  Per-lane source offsets inside a tile
+  // are fixed (dvo); the tile offset i*TILE is a scalar.
+  constexpr int NDMA = (NBLK + NW - 1) / NW;
   const int drow = lane / CPR, dch = lane % CPR;
+  int dvo[NDMA];
+#pragma unroll
+  for (int x = 0; x < NDMA; ++x) {
+    const int row = (wave + x * NW) * (1024 / ROWB) + drow;
+    dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
+  }
+  const auto qrs = make_rsrc(Qb, S * ROWB);
+  const auto dors = make_rsrc(dOb, S * ROWB);
+  const auto ors = make_rsrc(Ob, S * ROWB);
+  const auto lrs = make_rsrc(Lb, S * 4);
   auto dma_tile = [&](int i, unsigned char* buf) __attribute__((always_inline)) {
-    const size_t off = (size_t)i * TILE;
 #pragma unroll
-    for (int part = 0; part < 3; ++part) {
-      const unsigned char* g = (part == 0 ? Qb : (part == 1 ? dOb : Ob)) + off;
-#pragma unroll
-      for (int x = 0; x < (NBLK + NW - 1) / NW; ++x) {
-        const int blk = wave + x * NW;
-        if (NBLK % NW == 0 || blk < NBLK) {
-          const int row = blk * (1024 / ROWB) + drow;
-          __builtin_amdgcn_global_load_lds(g + row * ROWB + ((dch ^ bswz(row, CPR)) << 4),
-                                           (__attribute__((address_space(3))) void*)(buf + part * TILE + blk * 1024),
-                                           16, 0, 0);
-        }
+    for (int x = 0; x < NDMA; ++x) {
+      const int blk = wave + x * NW;
+      if (NBLK % NW == 0 || blk < NBLK) {
+        dma16(qrs, buf + blk * 1024, dvo[x], i * TILE);
+        dma16(dors, buf + TILE + blk * 1024, dvo[x], i * TILE);
+        dma16(ors, buf + 2 * TILE + blk * 1024, dvo[x], i * TILE);
       }
     }
 #pragma unroll
     for (int p = 0; p < (BMQ + 63) / 64; ++p) {
-      if (wave == p % NW && 64 * p + lane < BMQ)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned char*>(Lb + (size_t)i * BMQ + 64 * p + lane),
-                                         (__attribute__((address_space(3))) void*)(buf + 3 * TILE + 256 * p), 4, 0, 0);
+      if (wave == p % NW && 64 * p + lane < BMQ) dma4(lrs, buf + 3 * TILE + 256 * p, 4 * lane, 4 * (i * BMQ + 64 * p));
     }
   };
 
@@ -200,10 +210,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       const u32x4 a = lds_read16(buf + TILE, off);
       const u32x4 o = lds_read16(buf + 2 * TILE, off);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        acc += to_f32<E>(a[w] & 0xFFFFu) * to_f32<E>(o[w] & 0xFFFFu);
-        acc += to_f32<E>(a[w] >> 16) * to_f32<E>(o[w] >> 16);
-      }
+      for (int w = 0; w < 4; ++w) acc = dot_pair<E>(a[w], o[w], acc);
     }
 #pragma unroll
     for (int sh = 1; sh < TPR; sh <<= 1) acc += __shfl_xor(acc, sh, 64);
@@ -223,7 +230,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int t = 0; t < KT; ++t) {
-        const int o = to.opnd[t & 3] + 128 * (t >> 2) + 32 * qb * ROWB;
+        const int o = to.opnd[t] + 32 * qb * ROWB;
         s = mfma32<E>(lds_read16(Qs, o), kf[t], s);
         dp = mfma32<E>(lds_read16(dOs, o), vf[t], dp);
       }
@@ -360,10 +367,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       dof[t] = gload16(dr + 16 * t);
       const u32x4 o = gload16(orr + 16 * t);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        part += to_f32<E>(dof[t][w] & 0xFFFFu) * to_f32<E>(o[w] & 0xFFFFu);
-        part += to_f32<E>(dof[t][w] >> 16) * to_f32<E>(o[w] >> 16);
-      }
+      for (int w = 0; w < 4; ++w) part = dot_pair<E>(dof[t][w], o[w], part);
     }
     delta = halfwave_sum(part);
   }
@@ -376,22 +380,25 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
 
-  // DMA of the K and V tiles of key tile j (row-major, swizzled) into an LDS buffer.
+  // DMA of the K and V tiles of key tile j (row-major, swizzled) into an LDS buffer;
+  // per-lane source offsets are fixed (dvo), the tile offset j*TILE is a scalar.
+  constexpr int NDMA = (NBLK + NW - 1) / NW;
   const int drow = lane / CPR, dch = lane % CPR;
+  int dvo[NDMA];
+#pragma unroll
+  for (int x = 0; x < NDMA; ++x) {
+    const int row = (wave + x * NW) * (1024 / ROWB) + drow;
+    dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
+  }
+  const auto krs = make_rsrc(Kb, S * ROWB);
+  const auto vrs = make_rsrc(Vb, S * ROWB);
   auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
-    const size_t off = (size_t)j * TILE;
 #pragma unroll
-    for (int part = 0; part < 2; ++part) {
-      const unsigned char* g = (part == 0 ? Kb : Vb) + off;
-#pragma unroll
-      for (int x = 0; x < (NBLK + NW - 1) / NW; ++x) {
-        const int blk = wave + x * NW;
-        if (NBLK % NW == 0 || blk < NBLK) {
-          const int row = blk * (1024 / ROWB) + drow;
-          __builtin_amdgcn_global_load_lds(g + row * ROWB + ((dch ^ bswz(row, CPR)) << 4),
-                                           (__attribute__((address_space(3))) void*)(buf + part * TILE + blk * 1024),
-                                           16, 0, 0);
-        }
+    for (int x = 0; x < NDMA; ++x) {
+      const int blk = wave + x * NW;
+      if (NBLK % NW == 0 || blk < NBLK) {
+        dma16(krs, buf + blk * 1024, dvo[x], j * TILE);
+        dma16(vrs, buf + TILE + blk * 1024, dvo[x], j * TILE);
       }
     }
   };
@@ -412,7 +419,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int t = 0; t < KT; ++t) {
-        const int o = to.opnd[t & 3] + 128 * (t >> 2) + 32 * nb * ROWB;
+        const int o = to.opnd[t] + 32 * nb * ROWB;
         s = mfma32<E>(lds_read16(Ks, o), qf[t], s);
         dp = mfma32<E>(lds_read16(Vs, o), dof[t], dp);
       }

@@ -90,6 +90,20 @@ __device__ __forceinline__ float add_pair<F16>(uint32_t w, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
 }
 
+// acc + a.lo * b.lo + a.hi * b.hi for two packed 16-bit pairs (v_dot2c_f32_*).
+template <typename E>
+__device__ __forceinline__ float dot_pair(uint32_t a, uint32_t b, float acc);
+
+template <>
+__device__ __forceinline__ float dot_pair<BF16>(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc, false);
+}
+
+template <>
+__device__ __forceinline__ float dot_pair<F16>(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+}
+
 // One 16-bit element -> fp32.
 template <typename E>
 __device__ __forceinline__ float to_f32(uint32_t bits16);
@@ -155,6 +169,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int b
 // when these builtins appear inside the kernel's own lambdas.)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, unsigned char* lds, int voff, int soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// The same DMA for 4 bytes per lane (buffer_load_dword ... lds): lane L's word
+// lands at lds + 4 L.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rs, unsigned char* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
 }
 
 __device__ __forceinline__ u32x4 gload16(const uint16_t* p) {
