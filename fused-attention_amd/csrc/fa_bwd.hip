@@ -103,21 +103,24 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
                  uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
                  int B, int H, int S, float scale_log2, float sm_scale) {
+  static_assert(BMQ == 64, "a query tile is two 32-row blocks");
   constexpr int NW = BNK / 32;
   constexpr int NT = 64 * NW;
-  constexpr int KT = D / 16, DB = D / 32, QB = BMQ / 32;
+  constexpr int KT = D / 16, DB = D / 32;
   constexpr int ROWB = D * 2, CPR = ROWB / 16;
-  constexpr int TILE = BMQ * ROWB;              // bytes of one Q / dO / O tile
+  constexpr int TILE = BMQ * ROWB;                       // bytes of one Q / dO / O tile
   constexpr int NBLK = TILE / 1024;
-  constexpr int BUF = 3 * TILE + BMQ * 4;       // Q | dO | O | LSE
-  constexpr int TPR = NT / BMQ;                 // threads per row for Delta
+  constexpr int BUFA = (3 * TILE + BMQ * 4 + 1023) / 1024 * 1024;  // Q | dO | O | LSE
+  constexpr int NBUF = 3;
+  constexpr int TPR = NT / BMQ;                          // threads per row for Delta
   static_assert(TILE % 1024 == 0, "tiles are whole 1 KB DMA blocks");
   static_assert(TPR >= 1 && (CPR % TPR) == 0, "Delta split");
   const float NEG_INF = -__builtin_inff();
 
-  __shared__ __attribute__((aligned(1024))) unsigned char buf0[BUF];
-  __shared__ __attribute__((aligned(1024))) unsigned char buf1[BUF];
-  __shared__ __attribute__((aligned(16))) float delta_s[BMQ];
+  // three tile buffers: tile i is computed while tile i+1 has landed (its Delta
+  // is formed) and tile i+2 is in flight
+  __shared__ __attribute__((aligned(1024))) unsigned char bufs[NBUF * BUFA];
+  __shared__ __attribute__((aligned(16))) float delta_s[2][BMQ];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -140,7 +143,6 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int k0w = jt * BNK + 32 * wave;   // first key of this wave
   const int n = k0w + c;                  // this lane's key
   const bool active = k0w < S;            // wave-uniform; S is a multiple of 32
-
 
   // K, V rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
   u32x4 kf[KT], vf[KT];
@@ -173,7 +175,9 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const auto dors = make_rsrc(dOb, S * ROWB);
   const auto ors = make_rsrc(Ob, S * ROWB);
   const auto lrs = make_rsrc(Lb, S * 4);
-  auto dma_tile = [&](int i, unsigned char* buf) __attribute__((always_inline)) {
+  auto bufp = [&](int i) __attribute__((always_inline)) { return bufs + ((i - i0) % NBUF) * BUFA; };
+  auto dma_tile = [&](int i) __attribute__((always_inline)) {
+    unsigned char* buf = bufp(i);
 #pragma unroll
     for (int x = 0; x < NDMA; ++x) {
       const int blk = wave + x * NW;
@@ -183,10 +187,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
         dma16(ors, buf + 2 * TILE + blk * 1024, dvo[x], i * TILE);
       }
     }
-#pragma unroll
-    for (int p = 0; p < (BMQ + 63) / 64; ++p) {
-      if (wave == p % NW && 64 * p + lane < BMQ) dma4(lrs, buf + 3 * TILE + 256 * p, 4 * lane, 4 * (i * BMQ + 64 * p));
-    }
+    if (wave == 0) dma4(lrs, buf + 3 * TILE, 4 * lane, 4 * i * BMQ);
   };
 
   TileOffsets<ROWB> to;
@@ -199,8 +200,12 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     dk_acc[db] = f32x16{};
   }
 
-  // Delta for the tile in `buf`: TPR threads per row, chunk subsets, then shuffles
-  auto delta_phase = [&](const unsigned char* buf) __attribute__((always_inline)) {
+  // Per tile, once: -Delta into dl (TPR threads per row, chunk subsets, shuffles)
+  // and the tile's LSE slice rewritten in place as -LSE / c.  Both are then the
+  // initial accumulators of the dP and S products, so the MFMAs deliver
+  // dP - Delta and S - LSE/c directly.
+  const float inv_c = 1.0f / scale_log2;
+  auto delta_phase = [&](unsigned char* buf, float* dl) __attribute__((always_inline)) {
     const int row = tid / TPR, part = tid % TPR;
     float acc = 0.f;
 #pragma unroll
@@ -214,90 +219,135 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
 #pragma unroll
     for (int sh = 1; sh < TPR; sh <<= 1) acc += __shfl_xor(acc, sh, 64);
-    if (part == 0) delta_s[row] = acc;
-  };
-
-  auto compute = [&](const unsigned char* buf, int qtile0) __attribute__((always_inline)) {
-    const unsigned char* Qs = buf;
-    const unsigned char* dOs = buf + TILE;
-    const float* Ls = reinterpret_cast<const float*>(buf + 3 * TILE);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int qrow0 = qtile0 + 32 * qb;   // first query of this block
-      if (qrow0 + 31 < k0w) continue;       // every query precedes every key of the wave
-                                            // (always true for an inactive wave)
-      // S = Q K^T and dP = dO V^T: lane (c = key, hh), register g -> query qrow0 + acc_row(g)
-      f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const int o = to.opnd[t] + 32 * qb * ROWB;
-        s = mfma32<E>(lds_read16(Qs, o), kf[t], s);
-        dp = mfma32<E>(lds_read16(dOs, o), vf[t], dp);
-      }
-      float lse[16], dl[16];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int r = 32 * qb + 8 * gq + 4 * hh;
-        const f32x4 lv = *reinterpret_cast<const f32x4*>(Ls + r);
-        const f32x4 dv = *reinterpret_cast<const f32x4*>(delta_s + r);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lse[4 * gq + e] = lv[e];
-          dl[4 * gq + e] = dv[e];
-        }
-      }
-      const bool diag = (qrow0 == k0w);
-      float p[16], ds[16];
-#pragma unroll
-      for (int g = 0; g < 16; ++g) {
-        float x = s[g];
-        if (diag && c > acc_row(g, hh)) x = NEG_INF;
-        p[g] = fast_exp2(__builtin_fmaf(x, scale_log2, -lse[g]));
-        ds[g] = p[g] * (dp[g] - dl[g]);
-      }
-      u32x4 pk[2], dsk[2];
-#pragma unroll
-      for (int i1 = 0; i1 < 2; ++i1) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          pk[i1][q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
-          dsk[i1][q] = pack2<E>(ds[8 * i1 + 2 * q], ds[8 * i1 + 2 * q + 1]);
-        }
-      }
-      // dV^T += dO^T P, dK^T += Q^T dS (k-slots: queries 32qb + 16i1 + 8r2 + 4hh + 0..3)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-#pragma unroll
-        for (int i1 = 0; i1 < 2; ++i1) {
-          const int u = 2 * qb + i1;
-          dv_acc[db] = mfma32<E>(tr_read2(dOs, to.tr(db, u, 0), to.tr(db, u, 1)), pk[i1], dv_acc[db]);
-          dk_acc[db] = mfma32<E>(tr_read2(Qs, to.tr(db, u, 0), to.tr(db, u, 1)), dsk[i1], dk_acc[db]);
-        }
-      }
+    if (part == 0) {
+      dl[row] = -acc;
+      float* Ls = reinterpret_cast<float*>(buf + 3 * TILE);
+      Ls[row] = -Ls[row] * inv_c;
     }
   };
-  // ---- main loop over query tiles i0 .. nq-1
-  auto step = [&](int i, auto par_tag) __attribute__((always_inline)) {
-    constexpr bool P = decltype(par_tag)::value;
-    unsigned char* cur = P ? buf1 : buf0;
-    unsigned char* nxt = P ? buf0 : buf1;
-    if (i + 1 < nq) dma_tile(i + 1, nxt);
-    delta_phase(cur);
-    __syncthreads();
-    compute(cur, i * BMQ);
-    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
-    __syncthreads();
+
+  // Accumulator init for query block qb: register g <-> query row 32qb + acc_row(g),
+  // i.e. four float4 runs at rows 32qb + 8gq + 4hh
+  auto load_rows = [&](const float* src, int qb) __attribute__((always_inline)) {
+    f32x16 v;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(src + 32 * qb + 8 * gq + 4 * hh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * gq + e] = x[e];
+    }
+    return v;
   };
 
-  dma_tile(i0, buf0);
+  // S - LSE/c = Q_b K^T - LSE/c and dP - Delta = dO_b V^T - Delta for 32-row query
+  // block qb: lane (c = key, hh), register g -> query 32 qb + acc_row(g)
+  auto sd = [&](const unsigned char* buf, const float* dl, int qb, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
+    s = load_rows(reinterpret_cast<const float*>(buf + 3 * TILE), qb);
+    dp = load_rows(dl, qb);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int o = to.opnd[t] + 32 * qb * ROWB;
+      s = mfma32<E>(lds_read16(buf, o), kf[t], s);
+      dp = mfma32<E>(lds_read16(buf + TILE, o), vf[t], dp);
+    }
+  };
+  // P = exp2(c (S - LSE/c)) and dS = P (dP - Delta), packed as B operands; on the
+  // diagonal block keys past the query are masked
+  auto grad = [&](int qb, const f32x16& s, const f32x16& dp, bool diag, u32x4 (&pk)[2], u32x4 (&dsk)[2])
+      __attribute__((always_inline)) {
+    float p[16], ds[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      float x = s[g];
+      if (diag && c > acc_row(g, hh)) x = NEG_INF;
+      p[g] = fast_exp2(x * scale_log2);
+      ds[g] = p[g] * dp[g];
+    }
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        pk[i1][q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+        dsk[i1][q] = pack2<E>(ds[8 * i1 + 2 * q], ds[8 * i1 + 2 * q + 1]);
+      }
+  };
+  // dV^T += dO^T P, dK^T += Q^T dS (k-slots: queries 32qb + 16i1 + 8r2 + 4hh + 0..3)
+  auto wacc = [&](const unsigned char* buf, int qb, const u32x4 (&pk)[2], const u32x4 (&dsk)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+        const int u = 2 * qb + i1;
+        dv_acc[db] = mfma32<E>(tr_read2(buf + TILE, to.tr(db, u, 0), to.tr(db, u, 1)), pk[i1], dv_acc[db]);
+        dk_acc[db] = mfma32<E>(tr_read2(buf, to.tr(db, u, 0), to.tr(db, u, 1)), dsk[i1], dk_acc[db]);
+      }
+  };
+
+  // a tile wholly past this wave's keys: both blocks in straight-line order so the
+  // VALU of one block runs under the MFMAs of the other
+  auto tile_full = [&](unsigned char* buf, const float* dl) __attribute__((always_inline)) {
+    f32x16 s0, dp0, s1, dp1;
+    u32x4 pk0[2], dsk0[2], pk1[2], dsk1[2];
+    sd(buf, dl, 0, s0, dp0);
+    sd(buf, dl, 1, s1, dp1);
+    grad(0, s0, dp0, false, pk0, dsk0);
+    wacc(buf, 0, pk0, dsk0);
+    grad(1, s1, dp1, false, pk1, dsk1);
+    wacc(buf, 1, pk1, dsk1);
+  };
+  // a tile meeting this wave's keys: blocks before the keys are skipped (always,
+  // for an inactive wave), the block starting at the wave's first key is masked
+  // (a rolled loop: it runs for two tiles per workgroup, and unrolling it would
+  // merge both blocks' live state into one schedule)
+  auto tile_edge = [&](unsigned char* buf, const float* dl, int qtile0) __attribute__((always_inline)) {
+#pragma nounroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qrow0 = qtile0 + 32 * qb;
+      if (qrow0 + 31 < k0w) continue;
+      f32x16 s, dp;
+      u32x4 pk[2], dsk[2];
+      sd(buf, dl, qb, s, dp);
+      grad(qb, s, dp, qrow0 == k0w, pk, dsk);
+      wacc(buf, qb, pk, dsk);
+    }
+  };
+
+  // ---- main loop over query tiles i0 .. nq-1: at the top of iteration i tile
+  // i+1 has landed (one barrier makes it and Delta(i) visible), tile i+2 starts
+  // its DMA into the buffer tile i-1 used, tile i is computed, Delta(i+1) formed
+  dma_tile(i0);
+  if (i0 + 1 < nq) dma_tile(i0 + 1);
   __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
   __syncthreads();
+  delta_phase(bufp(i0), delta_s[i0 & 1]);
+  auto top = [&](int i) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+    if (i + 2 < nq) dma_tile(i + 2);
+  };
+  auto bottom = [&](int i) __attribute__((always_inline)) {
+    if (i + 1 < nq) delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
+  };
+  // the two tiles that meet this workgroup's keys, then the full tiles (one
+  // straight path per loop keeps the accumulators in place across iterations)
   int i = i0;
-  for (; i + 1 < nq; i += 2) {
-    step(i, BTag<false>{});
-    step(i + 1, BTag<true>{});
+  for (; i < nq && i < i0 + 2; ++i) {
+    top(i);
+    tile_edge(bufp(i), delta_s[i & 1], i * BMQ);
+    bottom(i);
   }
-  if (i < nq) step(i, BTag<false>{});
+  if (active) {
+    for (; i < nq; ++i) {
+      top(i);
+      tile_full(bufp(i), delta_s[i & 1]);
+      bottom(i);
+    }
+  } else {
+    for (; i < nq; ++i) {
+      top(i);
+      bottom(i);
+    }
+  }
 
   // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7
   if (!active) return;
