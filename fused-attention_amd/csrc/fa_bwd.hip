@@ -114,7 +114,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   constexpr int NBUF = 3;
   constexpr int TPR = NT / BMQ;                          // threads per row for Delta
   static_assert(TILE % 1024 == 0, "tiles are whole 1 KB DMA blocks");
-  static_assert(TPR >= 1 && (CPR % TPR) == 0, "Delta split");
+  static_assert(TPR == 4 && (CPR % TPR) == 0, "Delta: one lane quad per row");
   const float NEG_INF = -__builtin_inff();
 
   // three tile buffers: tile i is computed while tile i+1 has landed (its Delta
@@ -217,13 +217,13 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 #pragma unroll
       for (int w = 0; w < 4; ++w) acc = dot_pair<E>(a[w], o[w], acc);
     }
-#pragma unroll
-    for (int sh = 1; sh < TPR; sh <<= 1) acc += __shfl_xor(acc, sh, 64);
-    if (part == 0) {
-      dl[row] = -acc;
-      float* Ls = reinterpret_cast<float*>(buf + 3 * TILE);
-      Ls[row] = -Ls[row] * inv_c;
-    }
+    acc = quad_sum(acc);
+    // the four lanes of a row's quad store the same values (no branch, so this
+    // joins the surrounding MFMA schedule)
+    float* Ls = reinterpret_cast<float*>(buf + 3 * TILE);
+    const float lsc = -Ls[row] * inv_c;
+    dl[row] = -acc;
+    Ls[row] = lsc;
   };
 
   // Accumulator init for query block qb: register g <-> query row 32qb + acc_row(g),
@@ -337,10 +337,12 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     bottom(i);
   }
   if (active) {
+    // Delta(i+1) is formed first, in the same schedule as tile i's MFMAs; after
+    // the last tile it runs on the idle buffer and its result is never read
     for (; i < nq; ++i) {
       top(i);
+      delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
       tile_full(bufp(i), delta_s[i & 1]);
-      bottom(i);
     }
   } else {
     for (; i < nq; ++i) {

@@ -144,6 +144,13 @@ __device__ __forceinline__ float halfwave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Sum over the 4 lanes of a lane quad (DPP quad_perm [1,0,3,2] then [2,3,0,1]).
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+  return x;
+}
+
 __device__ __forceinline__ u32x4 lds_read16(const unsigned char* base, int byte_off) {
   return *reinterpret_cast<const u32x4*>(base + byte_off);
 }
