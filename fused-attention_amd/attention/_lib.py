@@ -34,6 +34,8 @@ SIGNATURES = {
     "fa_fwd": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _F, _I, _I, _VP]),
     "fa_bwd": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                     _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
+    "fa_bwd_gqa": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                        _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
     "fa_supported": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "fa_strerror": (ctypes.c_char_p, [_I]),
     "fa_version": (_I, []),
@@ -121,12 +123,20 @@ def fwd(q, k, v, o, lse, tile_m, tile_n):
 
 
 def bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n):
-    """Enqueue dK/dV then dQ on the current stream."""
+    """Enqueue dK/dV then dQ on the current stream (K/V may have fewer heads: GQA)."""
     lib = load()
     _require_device(q, k, v, o, do, lse, dq, dk, dv)
     B, H, S, D = q.shape
-    code = lib.fa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
-                      _ptr(dq), _ptr(dk), _ptr(dv), B, H, S, D, dtype_code(q.dtype),
-                      scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
-                      _stream(q.device))
-    check(code, "fa_bwd")
+    H_kv = k.shape[1]
+    if H_kv == H:
+        code = lib.fa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
+                          _ptr(dq), _ptr(dk), _ptr(dv), B, H, S, D, dtype_code(q.dtype),
+                          scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
+                          _stream(q.device))
+        check(code, "fa_bwd")
+        return
+    code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
+                          _ptr(dq), _ptr(dk), _ptr(dv), B, H, H_kv, S, D, dtype_code(q.dtype),
+                          scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
+                          _stream(q.device))
+    check(code, "fa_bwd_gqa")

@@ -91,14 +91,28 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
   fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
-  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, S, D, scale_log2, sm_scale, hip_stream};
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream};
+  return fn(a);
+}
+
+int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
+               const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+               int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+               int block_m, int block_n, void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, block_m, block_n);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
+  if (!fn) return FA_ERR_UNSUPPORTED;
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream};
   return fn(a);
 }
 
 int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with_lse, int is_bwd) {
   if (check_common(1, 1, 256, D, dtype, block_m, block_n) != FA_OK) return 0;
   if (group <= 0) return 0;
-  if (is_bwd) return (group == 1 && bwd_table(dtype, D, block_m, block_n)) ? 1 : 0;
+  if (is_bwd) return bwd_table(dtype, D, block_m, block_n) ? 1 : 0;
   return fwd_table(dtype, D, block_m, block_n, heads_per_wg(group, block_m, block_n), with_lse) ? 1 : 0;
 }
 
@@ -116,6 +130,6 @@ const char* fa_strerror(int status) {
   }
 }
 
-int fa_version(void) { return 100; }
+int fa_version(void) { return 110; }
 
 }  // extern "C"

@@ -102,7 +102,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
                  const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
                  uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
-                 int B, int H, int S, float scale_log2, float sm_scale) {
+                 int B, int H, int Hkv, int S, float scale_log2, float sm_scale) {
   static_assert(BMQ == 64, "a query tile is two 32-row blocks");
   constexpr int NW = BNK / 32;
   constexpr int NT = 64 * NW;
@@ -126,19 +126,19 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
 
-  // work item: (b, h, key tile), heaviest key tile (j = 0) first, XCD aware;
-  // the last key tile may be partial (S a multiple of 64, BNK = 128): waves whose
-  // keys start past S stay inactive but still share the DMA and the barriers
+  // work item: (b, K/V head, key tile), heaviest key tile (j = 0) first, XCD
+  // aware; the workgroup sums the contributions of the group's G = H / Hkv query
+  // heads (G = 1 for MHA) in its registers, so dK and dV are written once.  The
+  // last key tile may be partial (S a multiple of 64, BNK = 128): waves whose
+  // keys start past S stay inactive but still share the DMA and the barriers.
+  const int G = H / Hkv;
   const int nk = (S + BNK - 1) / BNK;
-  const int total = B * H * nk;
+  const int total = B * Hkv * nk;
   const int wg = blockIdx.x;
   const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
-  const int bh = L / nk, jt = L % nk;
-  const size_t base = (size_t)bh * S * D;
-  const unsigned char* Qb = reinterpret_cast<const unsigned char*>(Q + base);
-  const unsigned char* dOb = reinterpret_cast<const unsigned char*>(dO + base);
-  const unsigned char* Ob = reinterpret_cast<const unsigned char*>(O + base);
-  const float* Lb = Lse + (size_t)bh * S;
+  const int bkv = L / nk, jt = L % nk;     // bkv = b * Hkv + K/V head
+  const size_t base = (size_t)bkv * S * D;
+  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;   // first query head of the group
 
   const int k0w = jt * BNK + 32 * wave;   // first key of this wave
   const int n = k0w + c;                  // this lane's key
@@ -171,10 +171,8 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const int row = (wave + x * NW) * (1024 / ROWB) + drow;
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
-  const auto qrs = make_rsrc(Qb, S * ROWB);
-  const auto dors = make_rsrc(dOb, S * ROWB);
-  const auto ors = make_rsrc(Ob, S * ROWB);
-  const auto lrs = make_rsrc(Lb, S * 4);
+  // per query head of the group: Q, dO, O and LSE sources (set in the head loop)
+  __amdgpu_buffer_rsrc_t qrs, dors, ors, lrs;
   auto bufp = [&](int i) __attribute__((always_inline)) { return bufs + ((i - i0) % NBUF) * BUFA; };
   auto dma_tile = [&](int i) __attribute__((always_inline)) {
     unsigned char* buf = bufp(i);
@@ -315,11 +313,6 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // ---- main loop over query tiles i0 .. nq-1: at the top of iteration i tile
   // i+1 has landed (one barrier makes it and Delta(i) visible), tile i+2 starts
   // its DMA into the buffer tile i-1 used, tile i is computed, Delta(i+1) formed
-  dma_tile(i0);
-  if (i0 + 1 < nq) dma_tile(i0 + 1);
-  __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
-  __syncthreads();
-  delta_phase(bufp(i0), delta_s[i0 & 1]);
   auto top = [&](int i) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
@@ -328,26 +321,40 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   auto bottom = [&](int i) __attribute__((always_inline)) {
     if (i + 1 < nq) delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
   };
-  // the two tiles that meet this workgroup's keys, then the full tiles (one
-  // straight path per loop keeps the accumulators in place across iterations)
-  int i = i0;
-  for (; i < nq && i < i0 + 2; ++i) {
-    top(i);
-    tile_edge(bufp(i), delta_s[i & 1], i * BMQ);
-    bottom(i);
-  }
-  if (active) {
-    // Delta(i+1) is formed first, in the same schedule as tile i's MFMAs; after
-    // the last tile it runs on the idle buffer and its result is never read
-    for (; i < nq; ++i) {
+  for (int g = 0; g < G; ++g) {
+    const size_t hbase = (size_t)(bh0 + g) * S * D;
+    qrs = make_rsrc(Q + hbase, S * ROWB);
+    dors = make_rsrc(dO + hbase, S * ROWB);
+    ors = make_rsrc(O + hbase, S * ROWB);
+    lrs = make_rsrc(Lse + (size_t)(bh0 + g) * S, S * 4);
+    // every wave is done with the previous head's buffers before they refill
+    if (g > 0) __syncthreads();
+    dma_tile(i0);
+    if (i0 + 1 < nq) dma_tile(i0 + 1);
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+    delta_phase(bufp(i0), delta_s[i0 & 1]);
+    // the two tiles that meet this workgroup's keys, then the full tiles (one
+    // straight path per loop keeps the accumulators in place across iterations)
+    int i = i0;
+    for (; i < nq && i < i0 + 2; ++i) {
       top(i);
-      delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
-      tile_full(bufp(i), delta_s[i & 1]);
-    }
-  } else {
-    for (; i < nq; ++i) {
-      top(i);
+      tile_edge(bufp(i), delta_s[i & 1], i * BMQ);
       bottom(i);
+    }
+    if (active) {
+      // Delta(i+1) is formed first, in the same schedule as tile i's MFMAs; after
+      // the last tile it runs on the idle buffer and its result is never read
+      for (; i < nq; ++i) {
+        top(i);
+        delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
+        tile_full(bufp(i), delta_s[i & 1]);
+      }
+    } else {
+      for (; i < nq; ++i) {
+        top(i);
+        bottom(i);
+      }
     }
   }
 
@@ -382,7 +389,7 @@ __attribute__((amdgpu_waves_per_eu(dq_waves_per_simd<D, BM, BN>(), dq_waves_per_
 void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
                const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
-               uint16_t* __restrict__ dQ, int B, int H, int S, float scale_log2, float sm_scale) {
+               uint16_t* __restrict__ dQ, int B, int H, int Hkv, int S, float scale_log2, float sm_scale) {
   constexpr int NW = BM / 32;
   constexpr int NB = BN / 32, KT = D / 16, DB = D / 32;
   constexpr int ROWB = D * 2, CPR = ROWB / 16;
@@ -405,8 +412,10 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
   const int bh = L / nq, qt = nq - 1 - (L % nq);
   const size_t base = (size_t)bh * S * D;
-  const unsigned char* Kb = reinterpret_cast<const unsigned char*>(K + base);
-  const unsigned char* Vb = reinterpret_cast<const unsigned char*>(V + base);
+  // query head h reads K/V head h / (H / Hkv)
+  const size_t kvbase = (size_t)((bh / H) * Hkv + (bh % H) / (H / Hkv)) * S * D;
+  const unsigned char* Kb = reinterpret_cast<const unsigned char*>(K + kvbase);
+  const unsigned char* Vb = reinterpret_cast<const unsigned char*>(V + kvbase);
 
   const int r0 = qt * BM, q0 = r0 + 32 * wave, m = q0 + c;
   const int ntiles = (r0 + BM + BN - 1) / BN;
@@ -546,10 +555,10 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 // ---------------------------------------------------------------------------
 template <typename E, int D, int BMQ, int BNK>
 static bool launch_dkdv(const BwdArgs& a) {
-  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.H * ((a.S + BNK - 1) / BNK)), dim3(2 * BNK), 0,
+  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.Hkv * ((a.S + BNK - 1) / BNK)), dim3(2 * BNK), 0,
                      (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
-                     (uint16_t*)a.dk, (uint16_t*)a.dv, a.B, a.H, a.S, a.scale_log2, a.sm_scale);
+                     (uint16_t*)a.dk, (uint16_t*)a.dv, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -558,7 +567,7 @@ static bool launch_dq(const BwdArgs& a) {
   hipLaunchKernelGGL((dq_kernel<E, D, BM, BN>), dim3(a.B * a.H * (a.S / BM)), dim3(2 * BM), 0,
                      (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
-                     (uint16_t*)a.dq, a.B, a.H, a.S, a.scale_log2, a.sm_scale);
+                     (uint16_t*)a.dq, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
   return hipGetLastError() == hipSuccess;
 }
 

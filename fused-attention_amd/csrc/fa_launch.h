@@ -28,7 +28,7 @@ struct BwdArgs {
   void* dq;
   void* dk;
   void* dv;
-  int B, H, S, D;
+  int B, H, Hkv, S, D;
   float scale_log2;
   float sm_scale;
   void* stream;

@@ -76,6 +76,22 @@ FA_API int fa_bwd(const void* q, const void* k, const void* v, const void* o,
            int B, int H, int S, int D, int dtype, float scale_log2, float sm_scale,
            int block_m, int block_n, void* hip_stream);
 
+/*
+ * The same backward for grouped-query attention: q, o, d_o, dq are [B, H, S, D],
+ * k, v, dk, dv are [B, H_kv, S, D] with H_kv dividing H, lse is [B, H, S] from
+ * fa_fwd; query head h reads K/V head h / (H / H_kv).  dK and dV of a K/V head
+ * are the sums over its H / H_kv query heads, accumulated in one workgroup's
+ * registers (no atomics, each output element written once).
+ *
+ * No counterpart in the reference, whose backward is MHA-only (_check at
+ * attention/backward/fused_backward.py:154 rejects K/V of another head count);
+ * fa_bwd(...) equals fa_bwd_gqa(..., H_kv = H, ...).
+ */
+FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
+               const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+               int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+               int block_m, int block_n, void* hip_stream);
+
 /* 1 if a forward (with_lse 0/1) or backward (is_bwd 1) kernel exists for the
  * combination, else 0.  No reference counterpart: it lets a caller probe the
  * supported (dtype, D, tile) set before validating inputs. */

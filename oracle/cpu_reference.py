@@ -50,3 +50,14 @@ def reference_grads(q, k, v, do):
     o = reference_attention_explicit(q, k, v)
     o.backward(do.float())
     return o.detach(), q.grad, k.grad, v.grad
+
+
+def reference_grads_gqa(q, k, v, do):
+    """(O, dQ, dK, dV) from fp32 autograd of the explicit formula on K/V repeated to the
+    query heads (attention/gqa/reference_gqa.py:15-26): autograd of repeat_interleave sums
+    each group's gradients onto its K/V head."""
+    q, k, v = (t.detach().float().clone().requires_grad_(True) for t in (q, k, v))
+    g = q.shape[1] // k.shape[1]
+    o = reference_attention_explicit(q, k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1))
+    o.backward(do.float())
+    return o.detach(), q.grad, k.grad, v.grad

@@ -34,7 +34,7 @@ def test_library_exports_every_header_symbol(lib):
 def test_no_internal_symbols_leak():
     out = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
-    assert {"fa_fwd", "fa_bwd", "fa_supported", "fa_strerror", "fa_version"} <= exported
+    assert {"fa_fwd", "fa_bwd", "fa_bwd_gqa", "fa_supported", "fa_strerror", "fa_version"} <= exported
     assert not any(s.startswith("fa_fwd_table") or s.startswith("fa_bwd_table") for s in exported)
 
 
@@ -84,6 +84,25 @@ def test_bwd_rejects_bad_arguments(lib, kw, code):
     assert bwd(lib, **kw) == code
 
 
+def bwd_gqa(lib, B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE):
+    return lib.fa_bwd_gqa(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, B, H, Hkv, S, D, dtype, 0.1, 0.1,
+                          bm, bn, NULL)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(Hkv=3), _lib.FA_ERR_DIMS),
+    (dict(Hkv=0), _lib.FA_ERR_DIMS),
+    (dict(Hkv=8), _lib.FA_ERR_DIMS),
+    (dict(B=-1), _lib.FA_ERR_DIMS),
+    (dict(dtype=5), _lib.FA_ERR_DTYPE),
+    (dict(D=80), _lib.FA_ERR_HEADDIM),
+    (dict(S=200), _lib.FA_ERR_TILE),
+    (dict(ptr=NULL), _lib.FA_ERR_NULL),
+])
+def test_bwd_gqa_rejects_bad_arguments(lib, kw, code):
+    assert bwd_gqa(lib, **kw) == code
+
+
 def test_supported_table(lib):
     for dtype in (0, 1):
         for D in (32, 64, 128):
@@ -93,6 +112,7 @@ def test_supported_table(lib):
                     assert lib.fa_supported(dtype, D, bm, bn, 1, 1, 0) == 1
                     for group in (2, 4, 8, 32):
                         assert lib.fa_supported(dtype, D, bm, bn, group, 0, 0) == 1
+                        assert lib.fa_supported(dtype, D, bm, bn, group, 1, 1) == 1
     assert lib.fa_supported(1, 128, 64, 64, 0, 0, 0) == 0
     assert lib.fa_supported(1, 96, 64, 64, 1, 0, 0) == 0
 

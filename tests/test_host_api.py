@@ -92,6 +92,20 @@ def test_wrappers_raise_reference_errors_before_launch():
         fused_attention_autograd(q, q, q, 64, 64)
 
 
+def test_gqa_autograd_checks_before_launch():
+    from attention.gqa.fused_gqa import fused_gqa_attention_autograd
+    q = torch.zeros(1, 4, 128, 64, dtype=torch.float16)
+    kv = torch.zeros(1, 2, 128, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GQA needs"):
+        fused_gqa_attention_autograd(q, q[:, :3].contiguous(), q[:, :3].contiguous(), 64, 64)
+    with pytest.raises(ValueError, match="divisible"):
+        fused_gqa_attention_autograd(q, kv, kv, 128, 256)
+    with pytest.raises(TypeError):
+        fused_gqa_attention_autograd(q.float(), kv.float(), kv.float(), 64, 64)
+    with pytest.raises(ValueError, match="GPU"):
+        fused_gqa_attention_autograd(q, kv, kv, 64, 64)
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     from attention import _lib
     monkeypatch.setattr(_lib, "_lib", None)
