@@ -110,6 +110,13 @@ def check(code, what):
     raise RuntimeError(msg)
 
 
+def check_tiles(tile_m, tile_n):
+    """The kernels' tile contract: tile_m, tile_n in {64, 128}; N needs no relation to them
+    (a partial last tile is masked; the reference required N to be a multiple of both)."""
+    if tile_m not in (64, 128) or tile_n not in (64, 128):
+        raise ValueError(f"tile_m={tile_m} and tile_n={tile_n} must each be 64 or 128")
+
+
 def fwd(q, k, v, o, lse, tile_m, tile_n):
     """Enqueue the forward on the current stream.  Shapes already checked by the caller."""
     lib = load()

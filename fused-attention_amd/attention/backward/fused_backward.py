@@ -15,7 +15,8 @@ Backward = two atomic-free kernels on the same stream:
   inside both kernels from the O and dO rows they already read (the reference
   runs it as a separate torch op, :175).
 
-Shapes: q, k, v are (B, H, N, D) float16 or bfloat16, N divisible by both tiles.
+Shapes: q, k, v are (B, H, N, D) float16 or bfloat16, any N (a partial last tile
+is masked), tiles 64 or 128.
 Use:    o = fused_attention_autograd(q, k, v, tile_m=64, tile_n=64); o.backward(do)
 """
 
@@ -31,9 +32,7 @@ def _check(q, k, v, tile_m, tile_n):
         raise TypeError("q, k, v must all be float16 or all be bfloat16")
     if q.shape != k.shape or q.shape != v.shape or q.dim() != 4:
         raise ValueError(f"q, k, v must all be (B, H, N, D); got {q.shape}, {k.shape}, {v.shape}")
-    N = q.shape[2]
-    if N % tile_m or N % tile_n:
-        raise ValueError(f"N={N} must be divisible by tile_m={tile_m} and tile_n={tile_n}")
+    _lib.check_tiles(tile_m, tile_n)
 
 
 def _forward(q, k, v, tile_m, tile_n):

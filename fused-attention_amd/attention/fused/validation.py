@@ -1,16 +1,19 @@
 """Input checks shared by run_attention.py, the wrappers and the tests.
 
-Restates the reference contract (attention/fused/validation.py:1-87) with two
+Restates the reference contract (attention/fused/validation.py:1-87) with three
 widenings for this library:
   * dtypes: float16 and bfloat16 for the fused backend, and float32 as well for
     the fp32 reference backend (the reference accepts float16 only, :43-44);
-  * sequence length up to MAX_SEQ_LEN = 65536 (the reference stops at 8192, :17).
+  * sequence length up to MAX_SEQ_LEN = 65536 (the reference stops at 8192, :17);
+  * any N: the kernels mask a partial last tile (the reference requires N to be a
+    multiple of both tiles, :80-87, and lists partial edge tiles as future work);
+    the tiles themselves must be 64 or 128 (the kernels' tile set).
 
 Input requirements:
   Q: [B, H, N, D]   K: [B, H, N, D]   V: [B, H, N, D]   all contiguous, one dtype
   1 <= B <= 16, 1 <= H <= 32, 1 <= N <= 65536, D in {32, 64, 128}
   causal self-attention only, so Nq == Nk == N
-  N must be divisible by the query tile (block_m) and key tile (block_n)
+  query tile block_m and key tile block_n each 64 or 128
 
 Works on NumPy arrays and torch tensors (anything with .shape and .dtype).
 Every failure raises ValidationError naming the offending input and the
@@ -22,6 +25,7 @@ MAX_HEADS = 32
 MAX_SEQ_LEN = 65536
 SUPPORTED_HEAD_DIMS = (32, 64, 128)
 SUPPORTED_DTYPES = ("float16", "bfloat16", "float32")
+SUPPORTED_TILES = (64, 128)
 
 
 class ValidationError(ValueError):
@@ -66,12 +70,8 @@ def _check_bounds(B, H, N, D, block_m, block_n):
     if D not in SUPPORTED_HEAD_DIMS:
         raise ValidationError(f"head dim D={D} not supported; allowed {SUPPORTED_HEAD_DIMS}")
     for label, block in (("query tile block_m", block_m), ("key tile block_n", block_n)):
-        if block <= 0:
-            raise ValidationError(f"{label}={block} must be positive")
-        if N % block != 0:
-            raise ValidationError(
-                f"sequence length N={N} is not divisible by the {label}={block}; "
-                f"use N that is a multiple of {block} (partial edge tiles are not supported)")
+        if block not in SUPPORTED_TILES:
+            raise ValidationError(f"{label}={block} not supported; allowed {SUPPORTED_TILES}")
 
 
 def validate_qkv(q, k, v, block_m: int, block_n: int, dtypes=SUPPORTED_DTYPES) -> None:

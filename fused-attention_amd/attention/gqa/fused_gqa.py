@@ -27,8 +27,7 @@ def _check_gqa(q, k, v, tile_m, tile_n):
         raise ValueError(
             f"GQA needs K, V of shape [B, H_kv, N, D] with H_kv dividing H; got Q {tuple(q.shape)}, "
             f"K {tuple(k.shape)}, V {tuple(v.shape)}")
-    if N % tile_m != 0 or N % tile_n != 0:
-        raise ValueError(f"N={N} must be divisible by tile_m={tile_m} and tile_n={tile_n}")
+    _lib.check_tiles(tile_m, tile_n)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError(f"q, k, v must share one dtype; got {q.dtype}, {k.dtype}, {v.dtype}")
 

@@ -1,14 +1,15 @@
 """GQA/MQA input checks shared by run_attention_gqa.py and the GQA tests.
 
 Restates attention/gqa/validation_gqa.py:39-104 with the same widenings as
-attention/fused/validation.py (float16 / bfloat16 / float32, N <= 65536).
+attention/fused/validation.py (float16 / bfloat16 / float32, N <= 65536, any N,
+tiles 64 or 128).
 
 Input requirements:
   Q: [B, H, N, D]   K: [B, H_kv, N, D]   V: [B, H_kv, N, D]   contiguous, one dtype
   1 <= B <= 16, 1 <= H <= 32, 1 <= N <= 65536, D in {32, 64, 128}
   1 <= H_kv <= H and H % H_kv == 0   (H_kv == H is MHA, H_kv == 1 is MQA)
   query head h reads K/V head h // (H // H_kv)
-  N must be divisible by the query tile (block_m) and key tile (block_n)
+  query tile block_m and key tile block_n each 64 or 128
 """
 
 from attention.fused.validation import (MAX_BATCH, MAX_HEADS, MAX_SEQ_LEN,  # noqa: F401

@@ -55,8 +55,7 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
   if (B <= 0 || H <= 0 || S <= 0) return FA_ERR_DIMS;
   if (dtype != FA_F16 && dtype != FA_BF16) return FA_ERR_DTYPE;
   if (D != 32 && D != 64 && D != 128) return FA_ERR_HEADDIM;
-  if (!tile_ok(block_m) || !tile_ok(block_n)) return FA_ERR_TILE;
-  if (S % block_m != 0 || S % block_n != 0) return FA_ERR_TILE;
+  if (!tile_ok(block_m) || !tile_ok(block_n)) return FA_ERR_TILE;  // any S >= 1: partial edge tiles
   // element offsets inside one tensor are formed in 32-bit for the per-row
   // parts and 64-bit for the (batch, head) base; keep the whole tensor
   // addressable with 32-bit row indices
@@ -122,7 +121,7 @@ const char* fa_strerror(int status) {
     case FA_ERR_DIMS: return "invalid dimensions (B, H, H_kv, S must be positive and H_kv must divide H)";
     case FA_ERR_DTYPE: return "unsupported dtype (expected float16 or bfloat16)";
     case FA_ERR_HEADDIM: return "unsupported head dim (expected 32, 64 or 128)";
-    case FA_ERR_TILE: return "unsupported tile (block_m and block_n must be 64 or 128 and divide S)";
+    case FA_ERR_TILE: return "unsupported tile (block_m and block_n must be 64 or 128)";
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_UNSUPPORTED: return "no kernel for this combination";

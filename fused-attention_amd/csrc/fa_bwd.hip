@@ -129,8 +129,8 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // work item: (b, K/V head, key tile), heaviest key tile (j = 0) first, XCD
   // aware; the workgroup sums the contributions of the group's G = H / Hkv query
   // heads (G = 1 for MHA) in its registers, so dK and dV are written once.  The
-  // last key tile may be partial (S a multiple of 64, BNK = 128): waves whose
-  // keys start past S stay inactive but still share the DMA and the barriers.
+  // last key tile may be partial: waves whose keys start past S stay inactive but
+  // still share the DMA and the barriers, and lanes of keys past S are not stored.
   const int G = H / Hkv;
   const int nk = (S + BNK - 1) / BNK;
   const int total = B * Hkv * nk;
@@ -142,13 +142,13 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   const int k0w = jt * BNK + 32 * wave;   // first key of this wave
   const int n = k0w + c;                  // this lane's key
-  const bool active = k0w < S;            // wave-uniform; S is a multiple of 32
+  const bool active = k0w < S;            // wave-uniform
 
   // K, V rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
   u32x4 kf[KT], vf[KT];
   if (active) {
-    const uint16_t* kr = K + base + (size_t)n * D + 8 * hh;
-    const uint16_t* vr = V + base + (size_t)n * D + 8 * hh;
+    const uint16_t* kr = K + base + (size_t)min(n, S - 1) * D + 8 * hh;  // keys >= S: any valid row
+    const uint16_t* vr = V + base + (size_t)min(n, S - 1) * D + 8 * hh;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       kf[t] = gload16(kr + 16 * t);
@@ -156,7 +156,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
   }
 
-  const int nq = S / BMQ;
+  const int nq = (S + BMQ - 1) / BMQ;     // the last query tile may be partial
   const int i0 = (jt * BNK) / BMQ;        // first query tile that sees this key tile
 
   // DMA of the Q, dO and O tiles (row-major, swizzled) and the LSE slice of query
@@ -171,21 +171,42 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const int row = (wave + x * NW) * (1024 / ROWB) + drow;
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
-  // per query head of the group: Q, dO, O and LSE sources (set in the head loop)
-  __amdgpu_buffer_rsrc_t qrs, dors, ors, lrs;
-  auto bufp = [&](int i) __attribute__((always_inline)) { return bufs + ((i - i0) % NBUF) * BUFA; };
-  auto dma_tile = [&](int i) __attribute__((always_inline)) {
-    unsigned char* buf = bufp(i);
+  // The workgroup walks the (query tile, query head) pairs that meet its keys in
+  // one sequence, query tile major: pair t = (i0 + t / G, t % G), T pairs in all.
+  // One sequence rather than a loop per head keeps the three-buffer pipeline full
+  // across heads and leaves the tile loops un-nested.  Each tile's DMA uses
+  // descriptors sized to the rows below S, so rows of a partial last query tile
+  // read as zero (and contribute nothing: dO = 0 there).
+  const int NI = nq - i0;                 // query tiles that meet this key tile (>= 1)
+  const int T = G * NI;
+  const int TE = G * min(2, NI);          // pairs on the two tiles that meet the keys
+  // (the slot offset goes through readfirstlane as one scalar: left to itself the
+  // compiler splits t % NBUF into two terms and adds both to every LDS address)
+  auto bufp = [&](int t) __attribute__((always_inline)) {
+    return bufs + __builtin_amdgcn_readfirstlane((t % NBUF) * BUFA);
+  };
+  int di = i0, dg = 0;                    // the next pair to load, in sequence order
+  auto dma_next = [&](unsigned char* buf) __attribute__((always_inline)) {
+    const size_t row0 = (size_t)(bh0 + dg) * S + (size_t)di * BMQ;   // first row in [B, H, S]
+    const int rows = min(BMQ, S - di * BMQ);
+    const auto qrs = make_rsrc(Q + row0 * D, rows * ROWB);
+    const auto dors = make_rsrc(dO + row0 * D, rows * ROWB);
+    const auto ors = make_rsrc(O + row0 * D, rows * ROWB);
+    const auto lrs = make_rsrc(Lse + row0, rows * 4);
 #pragma unroll
     for (int x = 0; x < NDMA; ++x) {
       const int blk = wave + x * NW;
       if (NBLK % NW == 0 || blk < NBLK) {
-        dma16(qrs, buf + blk * 1024, dvo[x], i * TILE);
-        dma16(dors, buf + TILE + blk * 1024, dvo[x], i * TILE);
-        dma16(ors, buf + 2 * TILE + blk * 1024, dvo[x], i * TILE);
+        dma16(qrs, buf + blk * 1024, dvo[x], 0);
+        dma16(dors, buf + TILE + blk * 1024, dvo[x], 0);
+        dma16(ors, buf + 2 * TILE + blk * 1024, dvo[x], 0);
       }
     }
-    if (wave == 0) dma4(lrs, buf + 3 * TILE, 4 * lane, 4 * i * BMQ);
+    if (wave == 0) dma4(lrs, buf + 3 * TILE, 4 * lane, 0);
+    if (++dg == G) {
+      dg = 0;
+      ++di;
+    }
   };
 
   TileOffsets<ROWB> to;
@@ -310,56 +331,47 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
   };
 
-  // ---- main loop over query tiles i0 .. nq-1: at the top of iteration i tile
-  // i+1 has landed (one barrier makes it and Delta(i) visible), tile i+2 starts
-  // its DMA into the buffer tile i-1 used, tile i is computed, Delta(i+1) formed
-  auto top = [&](int i) __attribute__((always_inline)) {
+  // ---- main loop over the pairs: at the top of iteration t pair t+1 has landed
+  // (one barrier makes it and Delta(t) visible), pair t+2 starts its DMA into the
+  // buffer pair t-1 used, pair t is computed, Delta(t+1) formed
+  auto top = [&](int t) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
-    if (i + 2 < nq) dma_tile(i + 2);
+    if (t + 2 < T) dma_next(bufp(t + 2));
   };
-  auto bottom = [&](int i) __attribute__((always_inline)) {
-    if (i + 1 < nq) delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
+  auto bottom = [&](int t) __attribute__((always_inline)) {
+    if (t + 1 < T) delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
   };
-  for (int g = 0; g < G; ++g) {
-    const size_t hbase = (size_t)(bh0 + g) * S * D;
-    qrs = make_rsrc(Q + hbase, S * ROWB);
-    dors = make_rsrc(dO + hbase, S * ROWB);
-    ors = make_rsrc(O + hbase, S * ROWB);
-    lrs = make_rsrc(Lse + (size_t)(bh0 + g) * S, S * 4);
-    // every wave is done with the previous head's buffers before they refill
-    if (g > 0) __syncthreads();
-    dma_tile(i0);
-    if (i0 + 1 < nq) dma_tile(i0 + 1);
-    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
-    __syncthreads();
-    delta_phase(bufp(i0), delta_s[i0 & 1]);
-    // the two tiles that meet this workgroup's keys, then the full tiles (one
-    // straight path per loop keeps the accumulators in place across iterations)
-    int i = i0;
-    for (; i < nq && i < i0 + 2; ++i) {
-      top(i);
-      tile_edge(bufp(i), delta_s[i & 1], i * BMQ);
-      bottom(i);
+  dma_next(bufp(0));
+  if (T > 1) dma_next(bufp(1));
+  __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+  __syncthreads();
+  delta_phase(bufp(0), delta_s[0]);
+  // the pairs on the two tiles that meet this workgroup's keys, then the full tiles
+  // (one straight path per loop keeps the accumulators in place across iterations)
+  int t = 0;
+  for (; t < TE; ++t) {
+    top(t);
+    tile_edge(bufp(t), delta_s[t & 1], (i0 + (t >= G ? 1 : 0)) * BMQ);
+    bottom(t);
+  }
+  if (active) {
+    // Delta(t+1) is formed first, in the same schedule as pair t's MFMAs; after
+    // the last pair it runs on the idle buffer and its result is never read
+    for (; t < T; ++t) {
+      top(t);
+      delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
+      tile_full(bufp(t), delta_s[t & 1]);
     }
-    if (active) {
-      // Delta(i+1) is formed first, in the same schedule as tile i's MFMAs; after
-      // the last tile it runs on the idle buffer and its result is never read
-      for (; i < nq; ++i) {
-        top(i);
-        delta_phase(bufp(i + 1), delta_s[(i + 1) & 1]);
-        tile_full(bufp(i), delta_s[i & 1]);
-      }
-    } else {
-      for (; i < nq; ++i) {
-        top(i);
-        bottom(i);
-      }
+  } else {
+    for (; t < T; ++t) {
+      top(t);
+      bottom(t);
     }
   }
 
   // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7
-  if (!active) return;
+  if (!active || n >= S) return;
   uint16_t* dkr = dK + base + (size_t)n * D;
   uint16_t* dvr = dV + base + (size_t)n * D;
 #pragma unroll
@@ -406,7 +418,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int c = lane & 31, hh = lane >> 5;
 
   // work item: (b, h, query tile), heaviest (last) query tile first, XCD aware
-  const int nq = S / BM;
+  const int nq = (S + BM - 1) / BM;
   const int total = B * H * nq;
   const int wg = blockIdx.x;
   const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
@@ -418,7 +430,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const unsigned char* Vb = reinterpret_cast<const unsigned char*>(V + kvbase);
 
   const int r0 = qt * BM, q0 = r0 + 32 * wave, m = q0 + c;
-  const int ntiles = (r0 + BM + BN - 1) / BN;
+  const int ntiles = min((r0 + BM + BN - 1) / BN, (S + BN - 1) / BN);  // keys >= S are never needed
   const int jfull = r0 / BN;
 
 
@@ -426,9 +438,10 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   u32x4 qf[KT], dof[KT];
   float delta;
   {
-    const uint16_t* qr = Q + base + (size_t)m * D + 8 * hh;
-    const uint16_t* dr = dO + base + (size_t)m * D + 8 * hh;
-    const uint16_t* orr = O + base + (size_t)m * D + 8 * hh;
+    const size_t mr = (size_t)min(m, S - 1) * D;  // rows >= S: any valid row, never stored
+    const uint16_t* qr = Q + base + mr + 8 * hh;
+    const uint16_t* dr = dO + base + mr + 8 * hh;
+    const uint16_t* orr = O + base + mr + 8 * hh;
     float part = 0.f;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
@@ -440,7 +453,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
     delta = halfwave_sum(part);
   }
-  const float lse = Lse[(size_t)bh * S + m];
+  const float lse = Lse[(size_t)bh * S + min(m, S - 1)];
 
   TileOffsets<ROWB> to;
   to.init(lane);
@@ -459,15 +472,17 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const int row = (wave + x * NW) * (1024 / ROWB) + drow;
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
-  const auto krs = make_rsrc(Kb, S * ROWB);
-  const auto vrs = make_rsrc(Vb, S * ROWB);
+
   auto dma_tile = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+    const int rows_b = min(TILE, S * ROWB - j * TILE);  // rows of a partial last tile past S read zero
+    const auto krs = make_rsrc(Kb + (size_t)j * TILE, rows_b);
+    const auto vrs = make_rsrc(Vb + (size_t)j * TILE, rows_b);
 #pragma unroll
     for (int x = 0; x < NDMA; ++x) {
       const int blk = wave + x * NW;
       if (NBLK % NW == 0 || blk < NBLK) {
-        dma16(krs, buf + blk * 1024, dvo[x], j * TILE);
-        dma16(vrs, buf + TILE + blk * 1024, dvo[x], j * TILE);
+        dma16(krs, buf + blk * 1024, dvo[x], 0);
+        dma16(vrs, buf + TILE + blk * 1024, dvo[x], 0);
       }
     }
   };
@@ -544,6 +559,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     else step(j, BTag<false>{}, BTag<true>{});
   }
 
+  if (m >= S) return;
   uint16_t* dqr = dQ + base + (size_t)m * D;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -564,7 +580,7 @@ static bool launch_dkdv(const BwdArgs& a) {
 
 template <typename E, int D, int BM, int BN>
 static bool launch_dq(const BwdArgs& a) {
-  hipLaunchKernelGGL((dq_kernel<E, D, BM, BN>), dim3(a.B * a.H * (a.S / BM)), dim3(2 * BM), 0,
+  hipLaunchKernelGGL((dq_kernel<E, D, BM, BN>), dim3(a.B * a.H * ((a.S + BM - 1) / BM)), dim3(2 * BM), 0,
                      (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
                      (uint16_t*)a.dq, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);

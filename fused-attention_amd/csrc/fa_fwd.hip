@@ -124,7 +124,7 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int wh = wave % GH, wr = wave / GH;
 
   // ---- work item: (batch, head group, query tile), heavy first, XCD aware
-  const int nq = S / BM;
+  const int nq = (S + BM - 1) / BM;  // the last query tile may be partial
   const int units_per_b = H / GH;
   const int total = B * units_per_b * nq;
   const int wg = blockIdx.x;
@@ -143,7 +143,9 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int r0 = qt * BM;          // first query row of this workgroup
   const int q0 = r0 + wr * 32;     // first query row of this wave
   const int m = q0 + c;            // this lane's query row
-  const int ntiles = (r0 + BM + BN - 1) / BN;
+  // key tiles up to the workgroup's last row; keys >= S are never needed (each lies past
+  // every valid query, so the causal mask already excludes it)
+  const int ntiles = min((r0 + BM + BN - 1) / BN, (S + BN - 1) / BN);
   const int jfull = r0 / BN;       // tiles wholly below the workgroup's first row
 
   // ---- DMA of one K/V tile into an LDS buffer: 1 KB per wave instruction,
@@ -159,27 +161,32 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     kvo[i] = row * ROWB + (((dpos >> 4) ^ ((row * CPR / 16) & (CPR - 1))) << 4);
     vvo[i] = row * ROWB + (dpos ^ ((32 * (row & 3)) & (ROWB - 1)));
   }
-  const auto krs = make_rsrc(Kbh, S * ROWB);
-  const auto vrs = make_rsrc(Vbh, S * ROWB);
+  // one buffer descriptor per tile, sized to the rows below S: rows of a partial last
+  // tile past S read as zero (the scalar offset is not range-checked, the size is)
+  auto tile_rsrc = [&](const unsigned char* bh, int j) __attribute__((always_inline)) {
+    return make_rsrc(bh + (size_t)j * TILE, min(TILE, S * ROWB - j * TILE));
+  };
   auto dma_k = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+    const auto rs = tile_rsrc(Kbh, j);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int blk = wave + i * NW;
-      if (NBLK % NW == 0 || blk < NBLK) dma16(krs, buf + blk * 1024, kvo[i], j * TILE);
+      if (NBLK % NW == 0 || blk < NBLK) dma16(rs, buf + blk * 1024, kvo[i], 0);
     }
   };
   auto dma_v = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+    const auto rs = tile_rsrc(Vbh, j);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int blk = wave + i * NW;
-      if (NBLK % NW == 0 || blk < NBLK) dma16(vrs, buf + blk * 1024, vvo[i], j * TILE);
+      if (NBLK % NW == 0 || blk < NBLK) dma16(rs, buf + blk * 1024, vvo[i], 0);
     }
   };
 
   // ---- Q^T operand in registers: k-step t holds Q[m][16t + 8hh .. +7]
   u32x4 qf[KT];
   {
-    const uint16_t* qrow = Q + qbase + (size_t)m * D + 8 * hh;
+    const uint16_t* qrow = Q + qbase + (size_t)min(m, S - 1) * D + 8 * hh;  // rows >= S: any valid row
 #pragma unroll
     for (int t = 0; t < KT; ++t) qf[t] = gload16(qrow + 16 * t);
   }
@@ -376,21 +383,21 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const float ltot = halfwave_sum(lrun);
   const float inv = 1.0f / ltot;
   uint16_t* orow = O + qbase + (size_t)m * D;
+  if (m < S) {  // rows of a partial last query tile past S are not stored
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+    for (int db = 0; db < DB; ++db) {
 #pragma unroll
-    for (int i1 = 0; i1 < 2; ++i1) {
-      gstore16(orow + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, inv));
+      for (int i1 = 0; i1 < 2; ++i1) gstore16(orow + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, inv));
     }
+    if (LSE && hh == 0) Lse[(size_t)(b * H + hq) * S + m] = mrun + __log2f(ltot);
   }
-  if (LSE && hh == 0) Lse[(size_t)(b * H + hq) * S + m] = mrun + __log2f(ltot);
 }
 
 // ---------------------------------------------------------------------------
 template <typename E, int D, int BM, int BN, int GH, bool LSE>
 static int launch_fwd(const FwdArgs& a) {
   constexpr int NT = 64 * (BM / 32) * GH;
-  const int total = a.B * (a.H / GH) * (a.S / BM);
+  const int total = a.B * (a.H / GH) * ((a.S + BM - 1) / BM);
   hipLaunchKernelGGL((fwd_kernel<E, D, BM, BN, GH, LSE>), dim3(total), dim3(NT), 0, (hipStream_t)a.stream,
                      (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
                      (uint16_t*)a.o, a.lse, a.B, a.H, a.Hkv, a.S, a.scale_log2);

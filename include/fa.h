@@ -30,7 +30,7 @@ enum fa_status {
   FA_ERR_DIMS = -1,     /* B, H, H_kv or S not positive, or H % H_kv != 0 */
   FA_ERR_DTYPE = -2,    /* dtype is neither FA_F16 nor FA_BF16 */
   FA_ERR_HEADDIM = -3,  /* D not in {32, 64, 128} */
-  FA_ERR_TILE = -4,     /* block_m / block_n not in {64, 128} or not dividing S */
+  FA_ERR_TILE = -4,     /* block_m / block_n not in {64, 128} */
   FA_ERR_NULL = -5,     /* a required pointer is NULL */
   FA_ERR_LAUNCH = -6,   /* the HIP runtime rejected a launch */
   FA_ERR_UNSUPPORTED = -7 /* valid arguments, but no kernel for this combination */
@@ -51,8 +51,10 @@ enum fa_status {
  *        builds at attention/backward/fused_backward.py:169).
  * scale_log2 : log2(e) / sqrt(D) as the reference folds it (fused.py:74).
  * Query head h reads K/V head h / (H / H_kv) (fused_gqa.py:18).
- * block_m / block_n : query rows per head and keys per LDS tile, each in {64, 128},
- *        each dividing S (the reference's tile_m / tile_n contract, fused.py:70-71).
+ * block_m / block_n : query rows per head and keys per LDS tile, each in {64, 128}.
+ *        S may be any length >= 1: a partial last query or key tile is masked (the
+ *        reference requires S to be a multiple of both tiles, fused.py:70-71, and
+ *        names partial edge tiles as future work).
  */
 FA_API int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
            int B, int H, int H_kv, int S, int D, int dtype, float scale_log2,

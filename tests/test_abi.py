@@ -45,7 +45,9 @@ def test_strerror_covers_every_status(lib):
 
 
 NULL = ctypes.c_void_p(0)
-FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every case below fails validation first
+# never dereferenced: every case below fails argument validation before any launch (any S
+# is valid, so none of them may rely on S alone being rejected)
+FAKE = ctypes.c_void_p(0x1000)
 
 
 def fwd(lib, B=1, H=2, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE, lse=NULL):
@@ -66,7 +68,7 @@ def bwd(lib, B=1, H=2, S=256, D=64, dtype=0, bm=64, bn=64, ptr=FAKE):
     (dict(D=256), _lib.FA_ERR_HEADDIM),
     (dict(bm=32), _lib.FA_ERR_TILE),
     (dict(bn=256), _lib.FA_ERR_TILE),
-    (dict(S=192, bm=128), _lib.FA_ERR_TILE),
+    (dict(bm=96), _lib.FA_ERR_TILE),
     (dict(ptr=NULL), _lib.FA_ERR_NULL),
 ])
 def test_fwd_rejects_bad_arguments(lib, kw, code):
@@ -77,7 +79,7 @@ def test_fwd_rejects_bad_arguments(lib, kw, code):
     (dict(H=0), _lib.FA_ERR_DIMS),
     (dict(dtype=7), _lib.FA_ERR_DTYPE),
     (dict(D=96), _lib.FA_ERR_HEADDIM),
-    (dict(S=320, bn=128), _lib.FA_ERR_TILE),
+    (dict(bn=192), _lib.FA_ERR_TILE),
     (dict(ptr=NULL), _lib.FA_ERR_NULL),
 ])
 def test_bwd_rejects_bad_arguments(lib, kw, code):
@@ -96,7 +98,7 @@ def bwd_gqa(lib, B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE):
     (dict(B=-1), _lib.FA_ERR_DIMS),
     (dict(dtype=5), _lib.FA_ERR_DTYPE),
     (dict(D=80), _lib.FA_ERR_HEADDIM),
-    (dict(S=200), _lib.FA_ERR_TILE),
+    (dict(bm=256), _lib.FA_ERR_TILE),
     (dict(ptr=NULL), _lib.FA_ERR_NULL),
 ])
 def test_bwd_gqa_rejects_bad_arguments(lib, kw, code):

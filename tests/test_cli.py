@@ -77,7 +77,7 @@ def test_exit_codes(tmp_path, capsys):
     np.savez(inp, Q=q, K=k, V=v)
     assert run_attention.main(["--input", str(inp), "--output", str(out), "--backend", "hip"]) == 2
     assert "supported: float16" in capsys.readouterr().err
-    # tile that does not divide N
+    # a tile outside the kernels' set {64, 128}
     assert run_attention.main(["--input", str(inp), "--output", str(out), "--backend", "reference",
                                "--block-m", "96"]) == 2
     # NaN in the input gives a non-finite output -> runtime failure (1)

@@ -57,9 +57,8 @@ def test_row0_exact_and_prefix_mean_with_zero_q():
 @pytest.mark.parametrize("tiles", TILES, ids=lambda t: f"{t[0]}x{t[1]}")
 @pytest.mark.parametrize("case", cases.all_cases(), ids=lambda c: c.id)
 def test_reference_suite_fp16(case, tiles):
-    """The reference's 84 MHA cases (fp16, sigma tiny/large) at each tile config."""
-    if case.N % tiles[0] or case.N % tiles[1]:
-        pytest.skip("N not divisible by the tile")
+    """The reference's 84 MHA cases (fp16, sigma tiny/large) at each tile config (a case whose N
+    is not a multiple of a tile runs with a partial last tile, where the reference rejects it)."""
     q, k, v = (dev(x, torch.float16) for x in cases.make_inputs(case))
     log(f"suite {case.id} tiles={tiles}")
     o = fused_attention(q, k, v, *tiles)

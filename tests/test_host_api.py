@@ -50,14 +50,22 @@ def test_validate_rejections(mutate, msg):
     ((17, 1, 128, 64), 64, 64, "batch size"),
     ((1, 33, 128, 64), 64, 64, "head count"),
     ((1, 1, 128, 96), 64, 64, "head dim"),
-    ((1, 1, 192, 64), 128, 64, "divisible"),
-    ((1, 1, 128, 64), 0, 64, "positive"),
+    ((1, 1, 192, 64), 96, 64, "not supported"),
+    ((1, 1, 128, 64), 0, 64, "not supported"),
+    ((1, 1, 128, 64), 64, 32, "not supported"),
     ((1, 1, 2 * 65536, 32), 64, 64, "out of range"),
 ])
 def test_validate_bounds(shape, bm, bn, msg):
     q = type("T", (), {"shape": shape, "dtype": np.dtype(np.float16), "flags": {"C_CONTIGUOUS": True}})()
     with pytest.raises(ValidationError, match=msg):
         validate_qkv(q, q, q, bm, bn)
+
+
+def test_validate_accepts_any_sequence_length():
+    # partial edge tiles: N need not be a multiple of either tile (the reference required it)
+    for N in (1, 63, 100, 192, 4097):
+        validate_qkv(arr((1, 2, N, 64)), arr((1, 2, N, 64)), arr((1, 2, N, 64)), 128, 64)
+    assert validate_gqa(arr((1, 4, 100, 32)), arr((1, 2, 100, 32)), arr((1, 2, 100, 32)), 64, 128) == 2
 
 
 def test_validate_gqa_group_and_errors():
@@ -74,16 +82,17 @@ def test_validate_gqa_group_and_errors():
 
 def test_wrappers_raise_reference_errors_before_launch():
     q = torch.zeros(1, 2, 96, 64, dtype=torch.float16)
-    with pytest.raises(ValueError, match="divisible"):
-        fused_attention(q, q, q, 64, 64)
-    with pytest.raises(ValueError, match="divisible"):
-        fused_gqa_attention(q, q[:, :1], q[:, :1], 64, 64)
+    with pytest.raises(ValueError, match="64 or 128"):
+        fused_attention(q, q, q, 96, 64)
+    with pytest.raises(ValueError, match="64 or 128"):
+        fused_gqa_attention(q, q[:, :1], q[:, :1], 64, 32)
     with pytest.raises(ValueError, match="GQA needs"):
-        fused_gqa_attention(q, q[:, :, :64], q[:, :, :64], 32, 32)
+        fused_gqa_attention(q, q[:, :, :64], q[:, :, :64], 64, 64)
     with pytest.raises(TypeError):
-        _check(q.float(), q.float(), q.float(), 32, 32)
-    with pytest.raises(ValueError, match="divisible"):
-        _check(q, q, q, 64, 64)
+        _check(q.float(), q.float(), q.float(), 64, 64)
+    with pytest.raises(ValueError, match="64 or 128"):
+        _check(q, q, q, 64, 256)
+    _check(q, q, q, 128, 64)  # N = 96 is not a multiple of 128: fine, the edge tile is masked
     # on a CPU tensor the fused path refuses loudly instead of falling back
     q = torch.zeros(1, 2, 128, 64, dtype=torch.float16)
     with pytest.raises(ValueError, match="GPU"):
@@ -98,7 +107,7 @@ def test_gqa_autograd_checks_before_launch():
     kv = torch.zeros(1, 2, 128, 64, dtype=torch.float16)
     with pytest.raises(ValueError, match="GQA needs"):
         fused_gqa_attention_autograd(q, q[:, :3].contiguous(), q[:, :3].contiguous(), 64, 64)
-    with pytest.raises(ValueError, match="divisible"):
+    with pytest.raises(ValueError, match="64 or 128"):
         fused_gqa_attention_autograd(q, kv, kv, 128, 256)
     with pytest.raises(TypeError):
         fused_gqa_attention_autograd(q.float(), kv.float(), kv.float(), 64, 64)
@@ -142,5 +151,6 @@ def test_unfused_backends_match_oracle_on_cpu():
     q, k, v = _inputs(1, 4, 1, 64, 32, seed=6)
     np.testing.assert_allclose(unfused_gqa_attention(q, k, v, 64, 64).numpy(),
                                orc.forward(q.numpy(), k.numpy(), v.numpy()), atol=2e-5)
-    with pytest.raises(ValueError):
-        unfused_attention(q, q, q, 48, 64)
+    # the eager baseline has no tiles: any N, like the fused backends (here N = 64, tile 48)
+    np.testing.assert_allclose(unfused_attention(q, q, q, 48, 64).numpy(),
+                               orc.forward(q.numpy(), q.numpy(), q.numpy()), atol=2e-5)
