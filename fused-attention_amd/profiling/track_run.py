@@ -137,7 +137,10 @@ class Records:
 def collect_env(args):
     import torch
     props = torch.cuda.get_device_properties(0)
-    agent = sh("rocminfo")
+    # rocminfo lists the host CPU agents first: read the fields of the first GPU agent only
+    gpu_agents = [a for a in re.split(r"\n\*+\s*\nAgent \d+", sh("rocminfo"))
+                  if re.search(r"Name:\s+gfx", a)]
+    agent = gpu_agents[0] if gpu_agents else ""
     arch = re.findall(r"Name:\s+(gfx\d+\w*)", agent)
     cus = re.findall(r"Compute Unit:\s+(\d+)", agent)
     env = {
