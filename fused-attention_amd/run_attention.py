@@ -5,7 +5,7 @@
 Input:  .npz with contiguous arrays Q [B, H, N, D], K [B, H, N, D], V [B, H, N, D]
         float16 (all backends) or float32 (reference backend, or GPU backends with
         --compute-dtype); limits 1<=B<=16, 1<=H<=32, 1<=N<=65536, D in {32, 64, 128},
-        N divisible by --block-m and --block-n
+        --block-m and --block-n each 64 or 128 (any N: a partial last tile is masked)
 Output: .npy, float16 (or --output-dtype float32), shape [B, H, N, D]
 
 Backends:
