@@ -27,6 +27,7 @@ FA_ERR_TILE = -4
 FA_ERR_NULL = -5
 FA_ERR_LAUNCH = -6
 FA_ERR_UNSUPPORTED = -7
+FA_ERR_WORKSPACE = -8
 
 # (name, restype, argtypes) for every symbol of include/fa.h
 _VP, _I, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
@@ -35,7 +36,8 @@ SIGNATURES = {
     "fa_bwd": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                     _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
     "fa_bwd_gqa": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
-                        _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
+                        _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP, ctypes.c_size_t, _VP]),
+    "fa_bwd_gqa_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "fa_supported": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "fa_strerror": (ctypes.c_char_p, [_I]),
     "fa_version": (_I, []),
@@ -105,7 +107,7 @@ def check(code, what):
     msg = f"{what}: {strerror(code)} (status {code})"
     if code == FA_ERR_DTYPE:
         raise TypeError(msg)
-    if code in (FA_ERR_DIMS, FA_ERR_HEADDIM, FA_ERR_TILE, FA_ERR_NULL, FA_ERR_UNSUPPORTED):
+    if code in (FA_ERR_DIMS, FA_ERR_HEADDIM, FA_ERR_TILE, FA_ERR_NULL, FA_ERR_UNSUPPORTED, FA_ERR_WORKSPACE):
         raise ValueError(msg)
     raise RuntimeError(msg)
 
@@ -142,8 +144,13 @@ def bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n):
                           _stream(q.device))
         check(code, "fa_bwd")
         return
-    code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
-                          _ptr(dq), _ptr(dk), _ptr(dv), B, H, H_kv, S, D, dtype_code(q.dtype),
-                          scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
-                          _stream(q.device))
+    with torch.cuda.device(q.device):
+        # fp32 partial dK/dV when the K/V heads alone leave the GPU idle (MQA, few K/V
+        # heads); the caching allocator keeps the block for this stream's pending work
+        nbytes = lib.fa_bwd_gqa_workspace_size(B, H, H_kv, S, D)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+        code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
+                              _ptr(dq), _ptr(dk), _ptr(dv), B, H, H_kv, S, D, dtype_code(q.dtype),
+                              scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
+                              _ptr(ws), nbytes, _stream(q.device))
     check(code, "fa_bwd_gqa")

@@ -5,6 +5,8 @@
 // attention/backward/fused_backward.py:151-158); the Python layer raises the
 // reference's exception types before it ever reaches this ABI, so these
 // checks are the last line of defence for C callers.
+#include <cstdint>
+
 #include "fa_launch.h"
 
 namespace {
@@ -63,6 +65,36 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
   return FA_OK;
 }
 
+// Workgroups the dK/dV kernel should have for its heavy-first order to balance:
+// two rounds of one workgroup per CU (a split costs an fp32 partial write, read
+// and reduction, so it is kept to what load balance needs).
+int dkdv_target_workgroups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return 2 * cus;
+}
+
+size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
+  return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
+}
+
+// Head chunks per K/V head for the GQA dK/dV: the smallest divisor of the group
+// size G that gives at least the target number of workgroups (G itself if none
+// does); 1 when the group sums alone already fill the GPU or G = 1.
+int gqa_nsplit(int B, int H, int H_kv, int S) {
+  const int G = H / H_kv;
+  const long long items = (long long)B * H_kv * ((S + fa::kDkdvKeys - 1) / fa::kDkdvKeys);
+  const long long want = dkdv_target_workgroups();
+  int s = 1;
+  while (s < G && items * s < want) {
+    ++s;
+    while (G % s) ++s;
+  }
+  return s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -90,21 +122,39 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
   fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
-  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream};
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream,
+                nullptr, nullptr, 1};
   return fn(a);
+}
+
+size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D) {
+  if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
+  if (D != 32 && D != 64 && D != 128) return 0;
+  return gqa_workspace_bytes(B, H_kv, S, D, gqa_nsplit(B, H, H_kv, S));
 }
 
 int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
                const void* d_o, const float* lse, void* dq, void* dk, void* dv,
                int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
-               int block_m, int block_n, void* hip_stream) {
+               int block_m, int block_n, void* workspace, size_t workspace_bytes, void* hip_stream) {
   int st = check_common(B, H, S, D, dtype, block_m, block_n);
   if (st != FA_OK) return st;
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15)) return FA_ERR_WORKSPACE;
   fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
-  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream};
+  // the split the shape asks for, or the largest one the given workspace holds
+  const int G = H / H_kv;
+  int nsplit = workspace ? gqa_nsplit(B, H, H_kv, S) : 1;
+  while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > workspace_bytes) {
+    --nsplit;
+    while (G % nsplit) --nsplit;
+  }
+  float* wsk = nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
+  float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
+                wsk, wsv, nsplit};
   return fn(a);
 }
 
@@ -125,10 +175,11 @@ const char* fa_strerror(int status) {
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_UNSUPPORTED: return "no kernel for this combination";
+    case FA_ERR_WORKSPACE: return "workspace not 16-byte aligned";
     default: return "unknown status";
   }
 }
 
-int fa_version(void) { return 110; }
+int fa_version(void) { return 120; }
 
 }  // extern "C"

@@ -27,6 +27,8 @@
 // free: 16 consecutive rows read at one chunk (an MFMA operand read) land on 16
 // distinct 16-byte slots of the 256-byte bank line, and 4 consecutive rows read
 // as one 32-byte piece (a transposed read) land on 4 distinct 32-byte groups.
+#include <algorithm>
+
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -102,6 +104,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
                  const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
                  uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+                 float* __restrict__ Pk, float* __restrict__ Pv, int nsplit,
                  int B, int H, int Hkv, int S, float scale_log2, float sm_scale) {
   static_assert(BMQ == 64, "a query tile is two 32-row blocks");
   constexpr int NW = BNK / 32;
@@ -126,19 +129,23 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
 
-  // work item: (b, K/V head, key tile), heaviest key tile (j = 0) first, XCD
-  // aware; the workgroup sums the contributions of the group's G = H / Hkv query
-  // heads (G = 1 for MHA) in its registers, so dK and dV are written once.  The
-  // last key tile may be partial: waves whose keys start past S stay inactive but
-  // still share the DMA and the barriers, and lanes of keys past S are not stored.
+  // work item: (b, K/V head, head chunk, key tile), heaviest key tile (j = 0)
+  // first, XCD aware.  The workgroup sums the contributions of Gc = G / nsplit of
+  // the group's G = H / Hkv query heads in its registers (G = 1 for MHA): with
+  // nsplit = 1 dK and dV are written once, otherwise as fp32 partial sums per head
+  // chunk that gqa_reduce_kernel adds up.  The last key tile may be partial: waves
+  // whose keys start past S stay inactive but still share the DMA and the
+  // barriers, and lanes of keys past S are not stored.
   const int G = H / Hkv;
+  const int Gc = G / nsplit;
   const int nk = (S + BNK - 1) / BNK;
-  const int total = B * Hkv * nk;
+  const int total = B * Hkv * nsplit * nk;
   const int wg = blockIdx.x;
   const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
-  const int bkv = L / nk, jt = L % nk;     // bkv = b * Hkv + K/V head
+  const int u = L / nk, jt = L % nk;       // u = (b * Hkv + K/V head) * nsplit + head chunk
+  const int bkv = u / nsplit;              // b * Hkv + K/V head
   const size_t base = (size_t)bkv * S * D;
-  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;   // first query head of the group
+  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G + (u % nsplit) * Gc;   // first query head
 
   const int k0w = jt * BNK + 32 * wave;   // first key of this wave
   const int n = k0w + c;                  // this lane's key
@@ -172,14 +179,14 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
   // The workgroup walks the (query tile, query head) pairs that meet its keys in
-  // one sequence, query tile major: pair t = (i0 + t / G, t % G), T pairs in all.
+  // one sequence, query tile major: pair t = (i0 + t / Gc, t % Gc), T pairs in all.
   // One sequence rather than a loop per head keeps the three-buffer pipeline full
   // across heads and leaves the tile loops un-nested.  Each tile's DMA uses
   // descriptors sized to the rows below S, so rows of a partial last query tile
   // read as zero (and contribute nothing: dO = 0 there).
   const int NI = nq - i0;                 // query tiles that meet this key tile (>= 1)
-  const int T = G * NI;
-  const int TE = G * min(2, NI);          // pairs on the two tiles that meet the keys
+  const int T = Gc * NI;
+  const int TE = Gc * min(2, NI);         // pairs on the two tiles that meet the keys
   // (the slot offset goes through readfirstlane as one scalar: left to itself the
   // compiler splits t % NBUF into two terms and adds both to every LDS address)
   auto bufp = [&](int t) __attribute__((always_inline)) {
@@ -203,7 +210,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       }
     }
     if (wave == 0) dma4(lrs, buf + 3 * TILE, 4 * lane, 0);
-    if (++dg == G) {
+    if (++dg == Gc) {
       dg = 0;
       ++di;
     }
@@ -352,7 +359,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   int t = 0;
   for (; t < TE; ++t) {
     top(t);
-    tile_edge(bufp(t), delta_s[t & 1], (i0 + (t >= G ? 1 : 0)) * BMQ);
+    tile_edge(bufp(t), delta_s[t & 1], (i0 + (t >= Gc ? 1 : 0)) * BMQ);
     bottom(t);
   }
   if (active) {
@@ -372,6 +379,25 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7
   if (!active || n >= S) return;
+  if (nsplit > 1) {  // fp32 partial sums of this head chunk, dK already scaled
+    float* pkr = Pk + ((size_t)u * S + n) * D;
+    float* pvr = Pv + ((size_t)u * S + n) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+        const int d0 = db * 32 + 16 * i1 + 8 * hh;
+#pragma unroll
+        for (int h4 = 0; h4 < 2; ++h4) {
+          const int g0 = 8 * i1 + 4 * h4;
+          gstore_f32x4(pkr + d0 + 4 * h4, f32x4{dk_acc[db][g0] * sm_scale, dk_acc[db][g0 + 1] * sm_scale,
+                                                dk_acc[db][g0 + 2] * sm_scale, dk_acc[db][g0 + 3] * sm_scale});
+          gstore_f32x4(pvr + d0 + 4 * h4, f32x4{dv_acc[db][g0], dv_acc[db][g0 + 1], dv_acc[db][g0 + 2], dv_acc[db][g0 + 3]});
+        }
+      }
+    }
+    return;
+  }
   uint16_t* dkr = dK + base + (size_t)n * D;
   uint16_t* dvr = dV + base + (size_t)n * D;
 #pragma unroll
@@ -568,14 +594,57 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       gstore16(dqr + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, sm_scale));
 }
 
+// ===========================================================================
+// GQA/MQA dK / dV from per-head-chunk partial sums
+// ===========================================================================
+// dK[bkv, n, :] = sum over c < nsplit of Pk[bkv * nsplit + c, n, :] (and dV from
+// Pv), in chunk order, rounded once to the element type.  One thread per 8
+// consecutive d values; grid-stride over all B * Hkv * S * D / 8 of them.
+template <typename E, int D>
+__global__ __launch_bounds__(256)
+void gqa_reduce_kernel(const float* __restrict__ Pk, const float* __restrict__ Pv,
+                       uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int BHkv, int S, int nsplit) {
+  const size_t per_head = (size_t)S * (D / 8);
+  const size_t total = (size_t)BHkv * per_head;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const size_t bkv = i / per_head, r = i - bkv * per_head;
+    f32x16 acc = f32x16{};   // [0, 8) dK, [8, 16) dV
+    for (int c = 0; c < nsplit; ++c) {
+      const size_t off = ((bkv * nsplit + c) * per_head + r) * 8;
+      const f32x4 k0 = gload_f32x4(Pk + off), k1 = gload_f32x4(Pk + off + 4);
+      const f32x4 v0 = gload_f32x4(Pv + off), v1 = gload_f32x4(Pv + off + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] += k0[e];
+        acc[4 + e] += k1[e];
+        acc[8 + e] += v0[e];
+        acc[12 + e] += v1[e];
+      }
+    }
+    gstore16(dK + i * 8, pack8<E>(acc, 0, 1.0f));
+    gstore16(dV + i * 8, pack8<E>(acc, 8, 1.0f));
+  }
+}
+
 // ---------------------------------------------------------------------------
 template <typename E, int D, int BMQ, int BNK>
 static bool launch_dkdv(const BwdArgs& a) {
-  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.Hkv * ((a.S + BNK - 1) / BNK)), dim3(2 * BNK), 0,
-                     (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
+  static_assert(BNK == kDkdvKeys, "host split heuristics assume this key tile");
+  const int nsplit = a.nsplit > 1 ? a.nsplit : 1;
+  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.Hkv * nsplit * ((a.S + BNK - 1) / BNK)),
+                     dim3(2 * BNK), 0, (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
-                     (uint16_t*)a.dk, (uint16_t*)a.dv, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
-  return hipGetLastError() == hipSuccess;
+                     (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv, nsplit, a.B, a.H, a.Hkv, a.S,
+                     a.scale_log2, a.sm_scale);
+  if (hipGetLastError() != hipSuccess) return false;
+  if (nsplit > 1) {
+    const size_t threads = (size_t)a.B * a.Hkv * a.S * (D / 8);
+    const int grid = (int)std::min<size_t>((threads + 255) / 256, 8192);
+    hipLaunchKernelGGL((gqa_reduce_kernel<E, D>), dim3(grid), dim3(256), 0, (hipStream_t)a.stream,
+                       a.wsk, a.wsv, (uint16_t*)a.dk, (uint16_t*)a.dv, a.B * a.Hkv, a.S, nsplit);
+    if (hipGetLastError() != hipSuccess) return false;
+  }
+  return true;
 }
 
 template <typename E, int D, int BM, int BN>

@@ -191,6 +191,12 @@ __device__ __forceinline__ u32x4 gload16(const uint16_t* p) {
 __device__ __forceinline__ void gstore16(uint16_t* p, const u32x4& v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
+__device__ __forceinline__ void gstore_f32x4(float* p, const f32x4& v) {
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+__device__ __forceinline__ f32x4 gload_f32x4(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
 
 // ---------------------------------------------------------------------------
 // LDS tile layouts.

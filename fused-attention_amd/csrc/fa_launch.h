@@ -32,7 +32,16 @@ struct BwdArgs {
   float scale_log2;
   float sm_scale;
   void* stream;
+  // GQA/MQA: the H / Hkv query heads of a K/V head are summed by `nsplit`
+  // workgroups per key tile, each writing fp32 partial dK / dV ([B*Hkv*nsplit, S, D]
+  // each) that a reduction pass adds up; nsplit = 1: one workgroup, no workspace
+  float* wsk;
+  float* wsv;
+  int nsplit;
 };
+
+// keys per dK/dV workgroup (4 waves x 32 keys), for the split heuristics on the host
+constexpr int kDkdvKeys = 128;
 
 typedef int (*FwdFn)(const FwdArgs&);
 typedef int (*BwdFn)(const BwdArgs&);

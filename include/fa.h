@@ -19,6 +19,8 @@
 #define FA_API
 #endif
 
+#include <stddef.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -33,7 +35,8 @@ enum fa_status {
   FA_ERR_TILE = -4,     /* block_m / block_n not in {64, 128} */
   FA_ERR_NULL = -5,     /* a required pointer is NULL */
   FA_ERR_LAUNCH = -6,   /* the HIP runtime rejected a launch */
-  FA_ERR_UNSUPPORTED = -7 /* valid arguments, but no kernel for this combination */
+  FA_ERR_UNSUPPORTED = -7, /* valid arguments, but no kernel for this combination */
+  FA_ERR_WORKSPACE = -8    /* fa_bwd_gqa: workspace not 16-byte aligned */
 };
 
 /*
@@ -82,17 +85,30 @@ FA_API int fa_bwd(const void* q, const void* k, const void* v, const void* o,
  * The same backward for grouped-query attention: q, o, d_o, dq are [B, H, S, D],
  * k, v, dk, dv are [B, H_kv, S, D] with H_kv dividing H, lse is [B, H, S] from
  * fa_fwd; query head h reads K/V head h / (H / H_kv).  dK and dV of a K/V head
- * are the sums over its H / H_kv query heads, accumulated in one workgroup's
- * registers (no atomics, each output element written once).
+ * are the sums over its H / H_kv query heads, without atomics.
+ *
+ * workspace: NULL, or caller-owned device memory of workspace_bytes bytes,
+ * 16-byte aligned.  Without it one workgroup per key tile sums all H / H_kv query
+ * heads in registers, which leaves most of the GPU idle when B * H_kv * S / 128
+ * is small (MQA, few K/V heads).  With fa_bwd_gqa_workspace_size() bytes the
+ * heads are split over several workgroups that write fp32 partial sums into the
+ * workspace, and a reduction pass on the same stream adds them up (fixed order,
+ * deterministic).  A smaller workspace gets the largest split it holds.  The
+ * workspace must stay allocated until the stream has passed this call.
  *
  * No counterpart in the reference, whose backward is MHA-only (_check at
  * attention/backward/fused_backward.py:154 rejects K/V of another head count);
- * fa_bwd(...) equals fa_bwd_gqa(..., H_kv = H, ...).
+ * fa_bwd(...) equals fa_bwd_gqa(..., H_kv = H, ..., NULL, 0, stream).
  */
 FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
                const void* d_o, const float* lse, void* dq, void* dk, void* dv,
                int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
-               int block_m, int block_n, void* hip_stream);
+               int block_m, int block_n, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Workspace bytes fa_bwd_gqa uses for this shape on the current device (0: none,
+ * e.g. H_kv == H or enough K/V heads; 0 also for invalid dimensions).  No
+ * reference counterpart. */
+FA_API size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D);
 
 /* 1 if a forward (with_lse 0/1) or backward (is_bwd 1) kernel exists for the
  * combination, else 0.  No reference counterpart: it lets a caller probe the

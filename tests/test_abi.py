@@ -39,7 +39,7 @@ def test_no_internal_symbols_leak():
 
 
 def test_strerror_covers_every_status(lib):
-    for code in range(0, -8, -1):
+    for code in range(0, -9, -1):
         assert lib.fa_strerror(code).decode() not in ("", "unknown status")
     assert lib.fa_strerror(-99).decode() == "unknown status"
 
@@ -86,9 +86,9 @@ def test_bwd_rejects_bad_arguments(lib, kw, code):
     assert bwd(lib, **kw) == code
 
 
-def bwd_gqa(lib, B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE):
+def bwd_gqa(lib, B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE, ws=NULL, ws_bytes=0):
     return lib.fa_bwd_gqa(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, B, H, Hkv, S, D, dtype, 0.1, 0.1,
-                          bm, bn, NULL)
+                          bm, bn, ws, ws_bytes, NULL)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -100,9 +100,23 @@ def bwd_gqa(lib, B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE):
     (dict(D=80), _lib.FA_ERR_HEADDIM),
     (dict(bm=256), _lib.FA_ERR_TILE),
     (dict(ptr=NULL), _lib.FA_ERR_NULL),
+    (dict(ws=ctypes.c_void_p(0x1004), ws_bytes=1 << 20), _lib.FA_ERR_WORKSPACE),
 ])
 def test_bwd_gqa_rejects_bad_arguments(lib, kw, code):
     assert bwd_gqa(lib, **kw) == code
+
+
+def test_bwd_gqa_workspace_size(lib):
+    """fp32 partial dK and dV per head chunk: 2 * B * H_kv * nsplit * S * D * 4 bytes, with
+    nsplit the smallest divisor of the group giving 2 x 256 dK/dV workgroups (128 keys each)."""
+    ws = lib.fa_bwd_gqa_workspace_size
+    assert ws(2, 32, 32, 4096, 128) == 0                     # MHA: no split
+    assert ws(2, 32, 8, 4096, 128) == 0                      # 2*8*32 = 512 workgroups already
+    assert ws(1, 32, 1, 4096, 64) == 2 * 16 * 4096 * 64 * 4  # MQA: 32 key tiles x 16 chunks
+    assert ws(1, 32, 4, 8192, 128) == 2 * 4 * 2 * 8192 * 128 * 4
+    assert ws(1, 6, 2, 100, 32) == 2 * 2 * 3 * 100 * 32 * 4  # group of 3: every head apart
+    for bad in ((0, 4, 2, 256, 64), (1, 4, 3, 256, 64), (1, 4, 2, 0, 64), (1, 4, 2, 256, 48)):
+        assert ws(*bad) == 0
 
 
 def test_supported_table(lib):

@@ -127,3 +127,47 @@ def test_mqa_backward_full_size_B1_H32_Hkv1_S4096_D64_fp16():
     v = v * 0.5
     log("mqa-bwd full-size B1 H32 Hkv1 S4096 D64 fp16")
     check(q, k, v, do, (128, 64), "mqa-bwd B1H32Hkv1 S4096 D64")
+
+
+def _bwd_through_abi(q, k, v, o, do, lse, ws_bytes):
+    """dQ, dK, dV from fa_bwd_gqa with a workspace of ws_bytes (0: NULL, no head split)."""
+    import ctypes
+    import math
+    from attention import _lib
+    lib = _lib.load()
+    B, H, S, D = q.shape
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    code = lib.fa_bwd_gqa(*(ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv)),
+                          B, H, k.shape[1], S, D, _lib.dtype_code(q.dtype), _lib.scale_log2(D),
+                          1.0 / math.sqrt(D), 128, 64, _lib._ptr(ws), ws_bytes,
+                          _lib._stream(q.device))
+    _lib.check(code, "fa_bwd_gqa")
+    torch.cuda.synchronize()
+    return dq, dk, dv
+
+
+@pytest.mark.parametrize("shape", [(1, 32, 1, 1000, 64), (1, 8, 2, 777, 128), (2, 12, 4, 300, 32)],
+                         ids=lambda s: "B%dH%dHkv%dS%dD%d" % s)
+def test_gqa_head_split_matches_register_sums(shape):
+    """The split over head chunks (fp32 partials + reduction) against one workgroup summing every
+    head in registers: dQ identical, dK/dV equal up to fp32 summation order; a smaller workspace
+    takes a smaller split; repeated calls are bitwise reproducible."""
+    from attention import _lib
+    from attention.backward.fused_backward import _forward
+    B, H, Hkv, S, D = shape
+    q, k, v, do = make(B, H, Hkv, S, D, torch.bfloat16, seed=S + D)
+    o, lse = _forward(q, k, v, 128, 64)
+    need = _lib.load().fa_bwd_gqa_workspace_size(B, H, Hkv, S, D)
+    assert need > 0, "these shapes leave the GPU idle without a split"
+    log(f"gqa head split {shape} workspace {need} B")
+    ref = _bwd_through_abi(q, k, v, o, do, lse, 0)
+    got = _bwd_through_abi(q, k, v, o, do, lse, need)
+    assert torch.equal(got[0], ref[0])
+    for g, r in zip(got[1:], ref[1:]):
+        assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
+    again = _bwd_through_abi(q, k, v, o, do, lse, need)
+    assert all(torch.equal(a, b) for a, b in zip(got, again))
+    half = _bwd_through_abi(q, k, v, o, do, lse, need // 2)
+    for g, r in zip(half[1:], ref[1:]):
+        assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
