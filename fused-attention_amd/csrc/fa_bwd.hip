@@ -321,6 +321,107 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     grad(1, s1, dp1, false, pk1, dsk1);
     wacc(buf, 1, pk1, dsk1);
   };
+
+  // The same tile at D = 128 (one wave per SIMD, so nothing else hides its LDS
+  // latency), as eight regions pinned by sched_barrier: each issues the operand
+  // reads of the next region's 8 MFMAs while its own 8 MFMAs run, the P / dS math
+  // is spread over four of them in halves, and Delta of the next tile fills the
+  // last but one.  Same arithmetic in the same order as tile_full (bitwise equal),
+  // 7 % faster at the headline shape than the compiler's own schedule, whose
+  // MFMAs each waited for an operand read issued just before them.
+  constexpr int KH = KT / 2, DH = DB / 2;
+  auto rd_sd = [&](const unsigned char* buf, int qb, int half, u32x4 (&r)[2 * KH]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+      const int o = to.opnd[KH * half + i] + 32 * qb * ROWB;
+      r[i] = lds_read16(buf, o);
+      r[KH + i] = lds_read16(buf + TILE, o);
+    }
+  };
+  auto mm_sd = [&](int half, const u32x4 (&r)[2 * KH], f32x16& s, f32x16& dp) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+      s = mfma32<E>(r[i], kf[KH * half + i], s);
+      dp = mfma32<E>(r[KH + i], vf[KH * half + i], dp);
+    }
+  };
+  auto rd_w = [&](const unsigned char* buf, int qb, int half, u32x4 (&r)[2 * KH]) __attribute__((always_inline)) {
+    static_assert(D != 128 || 4 * DH == 2 * KH, "one operand buffer serves both phases");
+#pragma unroll
+    for (int j = 0; j < DH; ++j)
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+        const int db = DH * half + j, u = 2 * qb + i1;
+        r[2 * (2 * j + i1)] = tr_read2(buf + TILE, to.tr(db, u, 0), to.tr(db, u, 1));
+        r[2 * (2 * j + i1) + 1] = tr_read2(buf, to.tr(db, u, 0), to.tr(db, u, 1));
+      }
+  };
+  auto mm_w = [&](int half, const u32x4 (&r)[2 * KH], const u32x4 (&pk)[2], const u32x4 (&dsk)[2])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < DH; ++j)
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+        const int db = DH * half + j;
+        dv_acc[db] = mfma32<E>(r[2 * (2 * j + i1)], pk[i1], dv_acc[db]);
+        dk_acc[db] = mfma32<E>(r[2 * (2 * j + i1) + 1], dsk[i1], dk_acc[db]);
+      }
+  };
+  // P and dS of one half (registers 8 i1 .. 8 i1 + 7) of an unmasked block
+  auto grad_half = [&](int i1, const f32x16& s, const f32x16& dp, u32x4 (&pk)[2], u32x4 (&dsk)[2])
+      __attribute__((always_inline)) {
+    float p[8], ds[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      p[g] = fast_exp2(s[8 * i1 + g] * scale_log2);
+      ds[g] = p[g] * dp[8 * i1 + g];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pk[i1][q] = pack2<E>(p[2 * q], p[2 * q + 1]);
+      dsk[i1][q] = pack2<E>(ds[2 * q], ds[2 * q + 1]);
+    }
+  };
+  auto tile_full_pipelined = [&](unsigned char* buf, const float* dl, unsigned char* nbuf, float* ndl)
+      __attribute__((always_inline)) {
+    f32x16 s0, dp0, s1, dp1;
+    u32x4 pk0[2], dsk0[2], pk1[2], dsk1[2];
+    u32x4 ra[2 * KH], rb[2 * KH];
+    const float* lse_s = reinterpret_cast<const float*>(buf + 3 * TILE);
+    s0 = load_rows(lse_s, 0);
+    dp0 = load_rows(dl, 0);
+    rd_sd(buf, 0, 0, ra);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_sd(buf, 0, 1, rb);
+    mm_sd(0, ra, s0, dp0);
+    s1 = load_rows(lse_s, 1);
+    dp1 = load_rows(dl, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_sd(buf, 1, 0, ra);
+    mm_sd(1, rb, s0, dp0);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_sd(buf, 1, 1, rb);
+    mm_sd(0, ra, s1, dp1);
+    grad_half(0, s0, dp0, pk0, dsk0);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_w(buf, 0, 0, ra);
+    mm_sd(1, rb, s1, dp1);
+    grad_half(1, s0, dp0, pk0, dsk0);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_w(buf, 0, 1, rb);
+    mm_w(0, ra, pk0, dsk0);
+    grad_half(0, s1, dp1, pk1, dsk1);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_w(buf, 1, 0, ra);
+    mm_w(1, rb, pk0, dsk0);
+    grad_half(1, s1, dp1, pk1, dsk1);
+    __builtin_amdgcn_sched_barrier(0);
+    rd_w(buf, 1, 1, rb);
+    mm_w(0, ra, pk1, dsk1);
+    delta_phase(nbuf, ndl);
+    __builtin_amdgcn_sched_barrier(0);
+    mm_w(1, rb, pk1, dsk1);
+  };
   // a tile meeting this wave's keys: blocks before the keys are skipped (always,
   // for an inactive wave), the block starting at the wave's first key is masked
   // (a rolled loop: it runs for two tiles per workgroup, and unrolling it would
@@ -367,8 +468,12 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     // the last pair it runs on the idle buffer and its result is never read
     for (; t < T; ++t) {
       top(t);
-      delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
-      tile_full(bufp(t), delta_s[t & 1]);
+      if constexpr (D == 128) {
+        tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1]);
+      } else {
+        delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
+        tile_full(bufp(t), delta_s[t & 1]);
+      }
     }
   } else {
     for (; t < T; ++t) {
