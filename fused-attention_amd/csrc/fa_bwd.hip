@@ -169,7 +169,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // DMA of the Q, dO and O tiles (row-major, swizzled) and the LSE slice of query
   // tile i into an LDS buffer: waves take 1 KB blocks round-robin and lane L of a
   // block writes LDS bytes blk*1024 + 16L.  Per-lane source offsets inside a tile
-  // are fixed (dvo); the tile offset i*TILE is a scalar.
+  // are fixed (dvo); each tile gets its own buffer descriptor.
   constexpr int NDMA = (NBLK + NW - 1) / NW;
   const int drow = lane / CPR, dch = lane % CPR;
   int dvo[NDMA];
@@ -252,6 +252,32 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     Ls[row] = lsc;
   };
 
+  // delta_phase in two steps, so the pipelined tile below can issue the reads a
+  // region before the arithmetic
+  auto delta_load = [&](const unsigned char* buf, u32x4 (&da)[CPR / TPR], u32x4 (&dob)[CPR / TPR], float& ls)
+      __attribute__((always_inline)) {
+    const int row = tid / TPR, part = tid % TPR;
+#pragma unroll
+    for (int x = 0; x < CPR / TPR; ++x) {
+      const int off = row * ROWB + (((part + TPR * x) ^ bswz(row, CPR)) << 4);
+      da[x] = lds_read16(buf + TILE, off);
+      dob[x] = lds_read16(buf + 2 * TILE, off);
+    }
+    ls = reinterpret_cast<const float*>(buf + 3 * TILE)[row];
+  };
+  auto delta_store = [&](unsigned char* buf, float* dl, const u32x4 (&da)[CPR / TPR],
+                         const u32x4 (&dob)[CPR / TPR], float ls) __attribute__((always_inline)) {
+    const int row = tid / TPR;
+    float acc = 0.f;
+#pragma unroll
+    for (int x = 0; x < CPR / TPR; ++x)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc = dot_pair<E>(da[x][w], dob[x][w], acc);
+    acc = quad_sum(acc);
+    dl[row] = -acc;
+    reinterpret_cast<float*>(buf + 3 * TILE)[row] = -ls * inv_c;
+  };
+
   // Accumulator init for query block qb: register g <-> query row 32qb + acc_row(g),
   // i.e. four float4 runs at rows 32qb + 8gq + 4hh
   auto load_rows = [&](const float* src, int qb) __attribute__((always_inline)) {
@@ -323,12 +349,14 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   };
 
   // The same tile at D = 128 (one wave per SIMD, so nothing else hides its LDS
-  // latency), as eight regions pinned by sched_barrier: each issues the operand
-  // reads of the next region's 8 MFMAs while its own 8 MFMAs run, the P / dS math
-  // is spread over four of them in halves, and Delta of the next tile fills the
-  // last but one.  Same arithmetic in the same order as tile_full (bitwise equal),
-  // 7 % faster at the headline shape than the compiler's own schedule, whose
-  // MFMAs each waited for an operand read issued just before them.
+  // latency), as seven regions pinned by sched_barrier: each issues the operand
+  // reads of the next region's 8 MFMAs while its own 8 run, the P / dS math is spread
+  // over four of them in halves, the reads of the next tile's Delta go out a region
+  // before its arithmetic, and the last 8 dV/dK MFMAs (block 1, second half) move to
+  // the first region of the next tile, where they cover the reads that follow its
+  // barrier.  Same arithmetic in the same order as tile_full (bitwise equal); 12 %
+  // faster at the headline shape than the compiler's own schedule, whose MFMAs each
+  // waited for an operand read issued just before them.
   constexpr int KH = KT / 2, DH = DB / 2;
   auto rd_sd = [&](const unsigned char* buf, int qb, int half, u32x4 (&r)[2 * KH]) __attribute__((always_inline)) {
 #pragma unroll
@@ -382,7 +410,8 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       dsk[i1][q] = pack2<E>(ds[2 * q], ds[2 * q + 1]);
     }
   };
-  auto tile_full_pipelined = [&](unsigned char* buf, const float* dl, unsigned char* nbuf, float* ndl)
+  u32x4 c_r[2 * KH], c_pk[2], c_dsk[2];   // the deferred MFMAs' operands
+  auto tile_full_pipelined = [&](unsigned char* buf, const float* dl, unsigned char* nbuf, float* ndl, auto prev)
       __attribute__((always_inline)) {
     f32x16 s0, dp0, s1, dp1;
     u32x4 pk0[2], dsk0[2], pk1[2], dsk1[2];
@@ -391,6 +420,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     s0 = load_rows(lse_s, 0);
     dp0 = load_rows(dl, 0);
     rd_sd(buf, 0, 0, ra);
+    if constexpr (decltype(prev)::value) mm_w(1, c_r, c_pk, c_dsk);   // the previous tile's last MFMAs
     __builtin_amdgcn_sched_barrier(0);
     rd_sd(buf, 0, 1, rb);
     mm_sd(0, ra, s0, dp0);
@@ -415,12 +445,18 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     rd_w(buf, 1, 0, ra);
     mm_w(1, rb, pk0, dsk0);
     grad_half(1, s1, dp1, pk1, dsk1);
+    u32x4 da[CPR / TPR], dob[CPR / TPR];
+    float ls;
+    delta_load(nbuf, da, dob, ls);
     __builtin_amdgcn_sched_barrier(0);
-    rd_w(buf, 1, 1, rb);
+    rd_w(buf, 1, 1, c_r);
     mm_w(0, ra, pk1, dsk1);
-    delta_phase(nbuf, ndl);
-    __builtin_amdgcn_sched_barrier(0);
-    mm_w(1, rb, pk1, dsk1);
+    delta_store(nbuf, ndl, da, dob, ls);
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1) {
+      c_pk[i1] = pk1[i1];
+      c_dsk[i1] = dsk1[i1];
+    }
   };
   // a tile meeting this wave's keys: blocks before the keys are skipped (always,
   // for an inactive wave), the block starting at the wave's first key is masked
@@ -466,11 +502,19 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   if (active) {
     // Delta(t+1) is formed first, in the same schedule as pair t's MFMAs; after
     // the last pair it runs on the idle buffer and its result is never read
-    for (; t < T; ++t) {
-      top(t);
-      if constexpr (D == 128) {
-        tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1]);
-      } else {
+    if constexpr (D == 128) {
+      if (t < T) {
+        top(t);
+        tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1], BTag<false>{});
+        for (++t; t < T; ++t) {
+          top(t);
+          tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1], BTag<true>{});
+        }
+        mm_w(1, c_r, c_pk, c_dsk);
+      }
+    } else {
+      for (; t < T; ++t) {
+        top(t);
         delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
         tile_full(bufp(t), delta_s[t & 1]);
       }
