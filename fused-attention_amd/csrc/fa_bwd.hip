@@ -5,21 +5,28 @@
 //   dV = P^T dO              dP = dO V^T        Delta = rowsum(dO * O)
 //   dS = P * (dP - Delta)    dQ = dS K / sqrt(D)  dK = dS^T Q / sqrt(D)
 // Two kernels, launched in this order on the caller's stream:
-//   dkdv_kernel: one workgroup per key tile (tile_n keys, 32 per wave); loops over
-//                the query tiles (tile_m rows) at and below the diagonal.  Per query
-//                tile, Q, dO, O and LSE are copied global -> LDS by DMA (double
-//                buffered) and Delta is formed from the O and dO tiles in LDS.
-//                Each wave keeps its K and V rows in registers as MFMA B operands,
-//                computes S = Q K^T and dP = dO V^T with one lane per key, and
-//                accumulates dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and
-//                Q^T with ds_read_b64_tr_b16.
+//   dkdv_kernel: one workgroup per key tile (128 keys, 32 per wave) of one K/V
+//                head; walks the (64-row query tile, query head) pairs at and below
+//                the diagonal (G = H / Hkv heads per K/V head; 1 for MHA).  Per pair,
+//                Q, dO, O and LSE are copied global -> LDS by DMA (triple buffered)
+//                and Delta is formed from the O and dO tiles in LDS.  Each wave keeps
+//                its K and V rows in registers as MFMA B operands, computes S = Q K^T
+//                and dP = dO V^T with one lane per key, and accumulates
+//                dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and Q^T with
+//                ds_read_b64_tr_b16.  At D = 128 the full tiles run a hand-pipelined
+//                schedule (operand reads a region ahead of their MFMAs).
+//   gqa_reduce_kernel: only for GQA/MQA with a caller workspace, when the K/V heads
+//                alone would leave the GPU idle: the group's heads are then split
+//                over several dK/dV workgroups that write fp32 partial sums, and
+//                this pass adds them (fixed order) into dK and dV.
 //   dq_kernel:   one workgroup per query tile (tile_m rows, 32 per wave); loops over
 //                the key tiles (tile_n keys) up to the diagonal, heavy first.  Each
 //                wave keeps Q and dO rows in registers, computes S^T = K Q^T and
 //                dP^T = V dO^T with one lane per query (LSE and Delta are per-lane
 //                scalars; Delta comes from the O and dO rows in the prologue) and
 //                accumulates dQ^T += K^T dS^T, reading K^T with transposed reads.
-// Neither kernel uses atomics or a workspace; each output element is written once.
+// No kernel uses atomics; each output element is written once.  Any S >= 1: the
+// last query and key tiles may be partial (rows past S read as zero, never stored).
 //
 // LDS tiles are row-major with 16-byte chunk ch of row r stored at ch ^ bswz(r).
 // gfx950's LDS has 64 banks of 4 bytes and serves a 16-byte read 16 lanes per
