@@ -137,20 +137,20 @@ def bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n):
     _require_device(q, k, v, o, do, lse, dq, dk, dv)
     B, H, S, D = q.shape
     H_kv = k.shape[1]
-    if H_kv == H:
+    # (the size depends on the device only through its CU count, the same on every MI355X)
+    nbytes = lib.fa_bwd_gqa_workspace_size(B, H, H_kv, S, D)
+    if H_kv == H and nbytes == 0:
         code = lib.fa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
                           _ptr(dq), _ptr(dk), _ptr(dv), B, H, S, D, dtype_code(q.dtype),
                           scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
                           _stream(q.device))
         check(code, "fa_bwd")
         return
-    with torch.cuda.device(q.device):
-        # fp32 partial dK/dV when the K/V heads alone leave the GPU idle (MQA, few K/V
-        # heads); the caching allocator keeps the block for this stream's pending work
-        nbytes = lib.fa_bwd_gqa_workspace_size(B, H, H_kv, S, D)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
-        code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
-                              _ptr(dq), _ptr(dk), _ptr(dv), B, H, H_kv, S, D, dtype_code(q.dtype),
-                              scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
-                              _ptr(ws), nbytes, _stream(q.device))
+    # fp32 partial dK/dV when the key tiles alone leave the GPU idle (MQA, few heads,
+    # small batch); the caching allocator keeps the block for this stream's pending work
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
+                          _ptr(dq), _ptr(dk), _ptr(dv), B, H, H_kv, S, D, dtype_code(q.dtype),
+                          scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
+                          _ptr(ws), nbytes, _stream(q.device))
     check(code, "fa_bwd_gqa")

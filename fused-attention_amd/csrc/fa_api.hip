@@ -5,6 +5,7 @@
 // attention/backward/fused_backward.py:151-158); the Python layer raises the
 // reference's exception types before it ever reaches this ABI, so these
 // checks are the last line of defence for C callers.
+#include <atomic>
 #include <cstdint>
 
 #include "fa_launch.h"
@@ -67,12 +68,22 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
 
 // Workgroups the dK/dV kernel should have for its heavy-first order to balance:
 // two rounds of one workgroup per CU (a split costs an fp32 partial write, read
-// and reduction, so it is kept to what load balance needs).
+// and reduction, so it is kept to what load balance needs).  The CU count is
+// read once per device: the workspace query and the launch both ask on every
+// backward, and a short backward is bound by host time.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
 int dkdv_target_workgroups() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  int cus = (dev >= 0 && dev < kMaxDevices) ? g_cus[dev].load(std::memory_order_relaxed) : 0;
+  if (cus <= 0) {
+    if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    else if (dev < kMaxDevices)
+      g_cus[dev].store(cus, std::memory_order_relaxed);
+  }
   return 2 * cus;
 }
 
@@ -80,19 +91,24 @@ size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
   return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
 }
 
-// Head chunks per K/V head for the GQA dK/dV: the smallest divisor of the group
-// size G that gives at least the target number of workgroups (G itself if none
-// does); 1 when the group sums alone already fill the GPU or G = 1.
-int gqa_nsplit(int B, int H, int H_kv, int S) {
-  const int G = H / H_kv;
+// Chunks per key tile for dK/dV: enough that B * H_kv * (key tiles) * nsplit
+// reaches the target number of workgroups, at most the pairs of the heaviest key
+// tile (G query heads x all 64-row query tiles) and kMaxDkdvSplit; 1 when the key
+// tiles alone already fill the GPU, or when the heaviest tile has fewer than
+// kMinSplitPairs pairs: then the partial-sum traffic and the extra pass cost more
+// than the imbalance (measured: B=2 H=8 S=2048 D=128 0.133 ms whole, 0.146 ms split;
+// B=1 H=8 S=4096 0.241 -> 0.217 ms; MQA H=32 S=4096 3.17 -> 0.42 ms).
+constexpr int kMaxDkdvSplit = 64;
+constexpr int kMinSplitPairs = 64;
+int dkdv_nsplit(int B, int H, int H_kv, int S) {
   const long long items = (long long)B * H_kv * ((S + fa::kDkdvKeys - 1) / fa::kDkdvKeys);
   const long long want = dkdv_target_workgroups();
-  int s = 1;
-  while (s < G && items * s < want) {
-    ++s;
-    while (G % s) ++s;
-  }
-  return s;
+  const long long pairs = (long long)(H / H_kv) * ((S + 63) / 64);
+  if (items >= want || pairs < kMinSplitPairs) return 1;
+  long long s = (want + items - 1) / items;
+  if (s > pairs) s = pairs;
+  if (s > kMaxDkdvSplit) s = kMaxDkdvSplit;
+  return s < 1 ? 1 : (int)s;
 }
 
 }  // namespace
@@ -130,7 +146,7 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
 size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D) {
   if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
   if (D != 32 && D != 64 && D != 128) return 0;
-  return gqa_workspace_bytes(B, H_kv, S, D, gqa_nsplit(B, H, H_kv, S));
+  return gqa_workspace_bytes(B, H_kv, S, D, dkdv_nsplit(B, H, H_kv, S));
 }
 
 int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
@@ -145,12 +161,8 @@ int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
   fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
   // the split the shape asks for, or the largest one the given workspace holds
-  const int G = H / H_kv;
-  int nsplit = workspace ? gqa_nsplit(B, H, H_kv, S) : 1;
-  while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > workspace_bytes) {
-    --nsplit;
-    while (G % nsplit) --nsplit;
-  }
+  int nsplit = workspace ? dkdv_nsplit(B, H, H_kv, S) : 1;
+  while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > workspace_bytes) --nsplit;
   float* wsk = nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
   float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
@@ -180,6 +192,6 @@ const char* fa_strerror(int status) {
   }
 }
 
-int fa_version(void) { return 120; }
+int fa_version(void) { return 130; }
 
 }  // extern "C"

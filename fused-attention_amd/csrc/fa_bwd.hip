@@ -15,10 +15,10 @@
 //                dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and Q^T with
 //                ds_read_b64_tr_b16.  At D = 128 the full tiles run a hand-pipelined
 //                schedule (operand reads a region ahead of their MFMAs).
-//   gqa_reduce_kernel: only for GQA/MQA with a caller workspace, when the K/V heads
-//                alone would leave the GPU idle: the group's heads are then split
-//                over several dK/dV workgroups that write fp32 partial sums, and
-//                this pass adds them (fixed order) into dK and dV.
+//   dkdv_reduce_kernel: only with a caller workspace, when B * H_kv key tiles alone
+//                would leave the GPU idle (MQA, few heads): each key tile's pairs are
+//                then split over several dK/dV workgroups that write fp32 partial
+//                sums, and this pass adds them (fixed order) into dK and dV.
 //   dq_kernel:   one workgroup per query tile (tile_m rows, 32 per wave); loops over
 //                the key tiles (tile_n keys) up to the diagonal, heavy first.  Each
 //                wave keeps Q and dO rows in registers, computes S^T = K Q^T and
@@ -136,23 +136,23 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
 
-  // work item: (b, K/V head, head chunk, key tile), heaviest key tile (j = 0)
-  // first, XCD aware.  The workgroup sums the contributions of Gc = G / nsplit of
-  // the group's G = H / Hkv query heads in its registers (G = 1 for MHA): with
-  // nsplit = 1 dK and dV are written once, otherwise as fp32 partial sums per head
-  // chunk that gqa_reduce_kernel adds up.  The last key tile may be partial: waves
-  // whose keys start past S stay inactive but still share the DMA and the
-  // barriers, and lanes of keys past S are not stored.
+  // work item: (b, K/V head, chunk, key tile), heaviest key tile (j = 0) first,
+  // XCD aware.  A key tile meets T = G * NI (query tile, query head) pairs (G =
+  // H / Hkv query heads per K/V head, 1 for MHA); with nsplit = 1 one workgroup
+  // sums them all in its registers and writes dK and dV once, otherwise chunk c
+  // takes pairs [T c / nsplit, T (c+1) / nsplit) and writes fp32 partial sums that
+  // dkdv_reduce_kernel adds up.  The last key tile may be partial: waves whose keys
+  // start past S stay inactive but still share the DMA and the barriers, and lanes
+  // of keys past S are not stored.
   const int G = H / Hkv;
-  const int Gc = G / nsplit;
   const int nk = (S + BNK - 1) / BNK;
   const int total = B * Hkv * nsplit * nk;
   const int wg = blockIdx.x;
   const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
-  const int u = L / nk, jt = L % nk;       // u = (b * Hkv + K/V head) * nsplit + head chunk
+  const int u = L / nk, jt = L % nk;       // u = (b * Hkv + K/V head) * nsplit + chunk
   const int bkv = u / nsplit;              // b * Hkv + K/V head
   const size_t base = (size_t)bkv * S * D;
-  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G + (u % nsplit) * Gc;   // first query head
+  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;   // first query head of the group
 
   const int k0w = jt * BNK + 32 * wave;   // first key of this wave
   const int n = k0w + c;                  // this lane's key
@@ -185,21 +185,23 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const int row = (wave + x * NW) * (1024 / ROWB) + drow;
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
-  // The workgroup walks the (query tile, query head) pairs that meet its keys in
-  // one sequence, query tile major: pair t = (i0 + t / Gc, t % Gc), T pairs in all.
+  // The workgroup walks its chunk of the (query tile, query head) pairs that meet
+  // its keys in one sequence, query tile major: pair t = (i0 + t / G, t % G).
   // One sequence rather than a loop per head keeps the three-buffer pipeline full
   // across heads and leaves the tile loops un-nested.  Each tile's DMA uses
   // descriptors sized to the rows below S, so rows of a partial last query tile
   // read as zero (and contribute nothing: dO = 0 there).
   const int NI = nq - i0;                 // query tiles that meet this key tile (>= 1)
-  const int T = Gc * NI;
-  const int TE = Gc * min(2, NI);         // pairs on the two tiles that meet the keys
+  const int T = G * NI;
+  const int TE = G * min(2, NI);          // pairs on the two tiles that meet the keys
+  const int hc = u % nsplit;
+  const int tb = (int)((long long)T * hc / nsplit), te = (int)((long long)T * (hc + 1) / nsplit);
   // (the slot offset goes through readfirstlane as one scalar: left to itself the
   // compiler splits t % NBUF into two terms and adds both to every LDS address)
   auto bufp = [&](int t) __attribute__((always_inline)) {
     return bufs + __builtin_amdgcn_readfirstlane((t % NBUF) * BUFA);
   };
-  int di = i0, dg = 0;                    // the next pair to load, in sequence order
+  int di = i0 + tb / G, dg = tb % G;      // the next pair to load, in sequence order
   auto dma_next = [&](unsigned char* buf) __attribute__((always_inline)) {
     const size_t row0 = (size_t)(bh0 + dg) * S + (size_t)di * BMQ;   // first row in [B, H, S]
     const int rows = min(BMQ, S - di * BMQ);
@@ -217,7 +219,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       }
     }
     if (wave == 0) dma4(lrs, buf + 3 * TILE, 4 * lane, 0);
-    if (++dg == Gc) {
+    if (++dg == G) {
       dg = 0;
       ++di;
     }
@@ -488,46 +490,48 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   auto top = [&](int t) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
-    if (t + 2 < T) dma_next(bufp(t + 2));
+    if (t + 2 < te) dma_next(bufp(t + 2));
   };
   auto bottom = [&](int t) __attribute__((always_inline)) {
-    if (t + 1 < T) delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
+    if (t + 1 < te) delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
   };
-  dma_next(bufp(0));
-  if (T > 1) dma_next(bufp(1));
-  __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
-  __syncthreads();
-  delta_phase(bufp(0), delta_s[0]);
+  if (tb < te) {  // (a chunk of a light key tile can be empty: it stores zeros)
+    dma_next(bufp(tb));
+    if (tb + 1 < te) dma_next(bufp(tb + 1));
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+    delta_phase(bufp(tb), delta_s[tb & 1]);
+  }
   // the pairs on the two tiles that meet this workgroup's keys, then the full tiles
   // (one straight path per loop keeps the accumulators in place across iterations)
-  int t = 0;
-  for (; t < TE; ++t) {
+  int t = tb;
+  for (; t < min(te, TE); ++t) {
     top(t);
-    tile_edge(bufp(t), delta_s[t & 1], (i0 + (t >= Gc ? 1 : 0)) * BMQ);
+    tile_edge(bufp(t), delta_s[t & 1], (i0 + (t >= G ? 1 : 0)) * BMQ);
     bottom(t);
   }
   if (active) {
     // Delta(t+1) is formed first, in the same schedule as pair t's MFMAs; after
     // the last pair it runs on the idle buffer and its result is never read
     if constexpr (D == 128) {
-      if (t < T) {
+      if (t < te) {
         top(t);
         tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1], BTag<false>{});
-        for (++t; t < T; ++t) {
+        for (++t; t < te; ++t) {
           top(t);
           tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1], BTag<true>{});
         }
         mm_w(1, c_r, c_pk, c_dsk);
       }
     } else {
-      for (; t < T; ++t) {
+      for (; t < te; ++t) {
         top(t);
         delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
         tile_full(bufp(t), delta_s[t & 1]);
       }
     }
   } else {
-    for (; t < T; ++t) {
+    for (; t < te; ++t) {
       top(t);
       bottom(t);
     }
@@ -535,7 +539,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7
   if (!active || n >= S) return;
-  if (nsplit > 1) {  // fp32 partial sums of this head chunk, dK already scaled
+  if (nsplit > 1) {  // fp32 partial sums of this chunk, dK already scaled
     float* pkr = Pk + ((size_t)u * S + n) * D;
     float* pvr = Pv + ((size_t)u * S + n) * D;
 #pragma unroll
@@ -751,14 +755,14 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 }
 
 // ===========================================================================
-// GQA/MQA dK / dV from per-head-chunk partial sums
+// dK / dV from per-chunk partial sums
 // ===========================================================================
 // dK[bkv, n, :] = sum over c < nsplit of Pk[bkv * nsplit + c, n, :] (and dV from
 // Pv), in chunk order, rounded once to the element type.  One thread per 8
 // consecutive d values; grid-stride over all B * Hkv * S * D / 8 of them.
 template <typename E, int D>
 __global__ __launch_bounds__(256)
-void gqa_reduce_kernel(const float* __restrict__ Pk, const float* __restrict__ Pv,
+void dkdv_reduce_kernel(const float* __restrict__ Pk, const float* __restrict__ Pv,
                        uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int BHkv, int S, int nsplit) {
   const size_t per_head = (size_t)S * (D / 8);
   const size_t total = (size_t)BHkv * per_head;
@@ -796,7 +800,7 @@ static bool launch_dkdv(const BwdArgs& a) {
   if (nsplit > 1) {
     const size_t threads = (size_t)a.B * a.Hkv * a.S * (D / 8);
     const int grid = (int)std::min<size_t>((threads + 255) / 256, 8192);
-    hipLaunchKernelGGL((gqa_reduce_kernel<E, D>), dim3(grid), dim3(256), 0, (hipStream_t)a.stream,
+    hipLaunchKernelGGL((dkdv_reduce_kernel<E, D>), dim3(grid), dim3(256), 0, (hipStream_t)a.stream,
                        a.wsk, a.wsv, (uint16_t*)a.dk, (uint16_t*)a.dv, a.B * a.Hkv, a.S, nsplit);
     if (hipGetLastError() != hipSuccess) return false;
   }

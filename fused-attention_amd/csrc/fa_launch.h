@@ -32,9 +32,9 @@ struct BwdArgs {
   float scale_log2;
   float sm_scale;
   void* stream;
-  // GQA/MQA: the H / Hkv query heads of a K/V head are summed by `nsplit`
-  // workgroups per key tile, each writing fp32 partial dK / dV ([B*Hkv*nsplit, S, D]
-  // each) that a reduction pass adds up; nsplit = 1: one workgroup, no workspace
+  // the (query tile, query head) pairs of a key tile are split over `nsplit`
+  // workgroups, each writing fp32 partial dK / dV ([B*Hkv*nsplit, S, D] each) that a
+  // reduction pass adds up; nsplit = 1: one workgroup, no workspace
   float* wsk;
   float* wsv;
   int nsplit;

@@ -88,13 +88,15 @@ FA_API int fa_bwd(const void* q, const void* k, const void* v, const void* o,
  * are the sums over its H / H_kv query heads, without atomics.
  *
  * workspace: NULL, or caller-owned device memory of workspace_bytes bytes,
- * 16-byte aligned.  Without it one workgroup per key tile sums all H / H_kv query
- * heads in registers, which leaves most of the GPU idle when B * H_kv * S / 128
- * is small (MQA, few K/V heads).  With fa_bwd_gqa_workspace_size() bytes the
- * heads are split over several workgroups that write fp32 partial sums into the
- * workspace, and a reduction pass on the same stream adds them up (fixed order,
- * deterministic).  A smaller workspace gets the largest split it holds.  The
- * workspace must stay allocated until the stream has passed this call.
+ * 16-byte aligned.  Without it one workgroup per 128-key tile walks every (query
+ * tile, query head) pair of the tile and sums them in registers, which leaves most
+ * of the GPU idle when B * H_kv * S / 128 is small (MQA, few heads, small batch).
+ * With fa_bwd_gqa_workspace_size() bytes each key tile's pairs are split over
+ * several workgroups that write fp32 partial sums into the workspace, and a
+ * reduction pass on the same stream adds them up (fixed order, deterministic).  A
+ * smaller workspace gets the largest split it holds.  The workspace must stay
+ * allocated until the stream has passed this call.  H_kv = H (MHA) is accepted:
+ * that is how an MHA caller gets the split.
  *
  * No counterpart in the reference, whose backward is MHA-only (_check at
  * attention/backward/fused_backward.py:154 rejects K/V of another head count);
@@ -105,8 +107,8 @@ FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o
                int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
                int block_m, int block_n, void* workspace, size_t workspace_bytes, void* hip_stream);
 
-/* Workspace bytes fa_bwd_gqa uses for this shape on the current device (0: none,
- * e.g. H_kv == H or enough K/V heads; 0 also for invalid dimensions).  No
+/* Workspace bytes fa_bwd_gqa uses for this shape on the current device (0: none
+ * wanted, the key tiles alone fill the GPU; 0 also for invalid dimensions).  No
  * reference counterpart. */
 FA_API size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D);
 

@@ -147,12 +147,14 @@ def _bwd_through_abi(q, k, v, o, do, lse, ws_bytes):
     return dq, dk, dv
 
 
-@pytest.mark.parametrize("shape", [(1, 32, 1, 1000, 64), (1, 8, 2, 777, 128), (2, 12, 4, 300, 32)],
+@pytest.mark.parametrize("shape", [(1, 32, 1, 1000, 64), (1, 8, 2, 2000, 128), (2, 12, 4, 1500, 32),
+                                   (1, 4, 4, 4200, 128), (1, 2, 2, 4097, 64)],
                          ids=lambda s: "B%dH%dHkv%dS%dD%d" % s)
-def test_gqa_head_split_matches_register_sums(shape):
-    """The split over head chunks (fp32 partials + reduction) against one workgroup summing every
-    head in registers: dQ identical, dK/dV equal up to fp32 summation order; a smaller workspace
-    takes a smaller split; repeated calls are bitwise reproducible."""
+def test_dkdv_split_matches_register_sums(shape):
+    """The split of each key tile's (query tile, query head) pairs over several workgroups (fp32
+    partials + reduction; MHA and GQA) against one workgroup summing every pair in registers:
+    dQ identical, dK/dV equal up to fp32 summation order; a smaller workspace takes a smaller
+    split; repeated calls are bitwise reproducible."""
     from attention import _lib
     from attention.backward.fused_backward import _forward
     B, H, Hkv, S, D = shape
@@ -160,10 +162,16 @@ def test_gqa_head_split_matches_register_sums(shape):
     o, lse = _forward(q, k, v, 128, 64)
     need = _lib.load().fa_bwd_gqa_workspace_size(B, H, Hkv, S, D)
     assert need > 0, "these shapes leave the GPU idle without a split"
+    if Hkv == H:  # MHA: also the reference-compatible entry point without a workspace
+        from attention.backward.fused_backward import _backward
+        mha = _backward(q, k, v, o, lse, do, 128, 64)
+        torch.cuda.synchronize()
     log(f"gqa head split {shape} workspace {need} B")
     ref = _bwd_through_abi(q, k, v, o, do, lse, 0)
     got = _bwd_through_abi(q, k, v, o, do, lse, need)
     assert torch.equal(got[0], ref[0])
+    if Hkv == H:  # the Python layer takes the split for this shape
+        assert all(torch.equal(a, b) for a, b in zip(mha, got))
     for g, r in zip(got[1:], ref[1:]):
         assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
     again = _bwd_through_abi(q, k, v, o, do, lse, need)
