@@ -132,22 +132,19 @@ def fwd(q, k, v, o, lse, tile_m, tile_n):
 
 
 def bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n):
-    """Enqueue dK/dV then dQ on the current stream (K/V may have fewer heads: GQA)."""
+    """Enqueue the backward on the current stream (K/V may have fewer heads: GQA).
+
+    Goes through fa_bwd_gqa with its workspace (H_kv = H included): the per-row -LSE/c and
+    -Delta that let dQ run first and spare dK/dV forming Delta per key tile, plus fp32 partial
+    dK/dV when the key tiles alone leave the GPU idle (MQA, few heads, small batch).  The
+    caching allocator keeps the block for this stream's pending work.
+    """
     lib = load()
     _require_device(q, k, v, o, do, lse, dq, dk, dv)
     B, H, S, D = q.shape
     H_kv = k.shape[1]
     # (the size depends on the device only through its CU count, the same on every MI355X)
     nbytes = lib.fa_bwd_gqa_workspace_size(B, H, H_kv, S, D)
-    if H_kv == H and nbytes == 0:
-        code = lib.fa_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
-                          _ptr(dq), _ptr(dk), _ptr(dv), B, H, S, D, dtype_code(q.dtype),
-                          scale_log2(D), 1.0 / math.sqrt(D), int(tile_m), int(tile_n),
-                          _stream(q.device))
-        check(code, "fa_bwd")
-        return
-    # fp32 partial dK/dV when the key tiles alone leave the GPU idle (MQA, few heads,
-    # small batch); the caching allocator keeps the block for this stream's pending work
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
     code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),
                           _ptr(dq), _ptr(dk), _ptr(dv), B, H, H_kv, S, D, dtype_code(q.dtype),

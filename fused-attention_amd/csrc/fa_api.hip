@@ -91,6 +91,12 @@ size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
   return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
 }
 
+// -LSE/c and -Delta per query row ([2, B*H, S] fp32), rounded up to 256 bytes so
+// the partial sums after them stay aligned
+size_t rowb_bytes(int B, int H, int S) {
+  return (2 * (size_t)B * H * S * sizeof(float) + 255) / 256 * 256;
+}
+
 // Chunks per key tile for dK/dV: enough that B * H_kv * (key tiles) * nsplit
 // reaches the target number of workgroups, at most the pairs of the heaviest key
 // tile (G query heads x all 64-row query tiles) and kMaxDkdvSplit; 1 when the key
@@ -139,14 +145,14 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
   fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream,
-                nullptr, nullptr, 1};
+                nullptr, nullptr, 1, nullptr};
   return fn(a);
 }
 
 size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D) {
   if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
   if (D != 32 && D != 64 && D != 128) return 0;
-  return gqa_workspace_bytes(B, H_kv, S, D, dkdv_nsplit(B, H, H_kv, S));
+  return rowb_bytes(B, H, S) + gqa_workspace_bytes(B, H_kv, S, D, dkdv_nsplit(B, H, H_kv, S));
 }
 
 int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
@@ -160,13 +166,23 @@ int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15)) return FA_ERR_WORKSPACE;
   fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
-  // the split the shape asks for, or the largest one the given workspace holds
+  // the workspace holds, in this order and as far as it reaches: the per-row terms
+  // (dQ then runs first and dK/dV reads Delta instead of forming it), then the
+  // partial sums of the split the shape asks for, or of the largest one that fits
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  size_t left = workspace ? workspace_bytes : 0;
+  float* rowb = nullptr;
+  if (left >= rowb_bytes(B, H, S)) {
+    rowb = reinterpret_cast<float*>(ws);
+    ws += rowb_bytes(B, H, S);
+    left -= rowb_bytes(B, H, S);
+  }
   int nsplit = workspace ? dkdv_nsplit(B, H, H_kv, S) : 1;
-  while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > workspace_bytes) --nsplit;
-  float* wsk = nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
+  while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > left) --nsplit;
+  float* wsk = nsplit > 1 ? reinterpret_cast<float*>(ws) : nullptr;
   float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
-                wsk, wsv, nsplit};
+                wsk, wsv, nsplit, rowb};
   return fn(a);
 }
 
@@ -192,6 +208,6 @@ const char* fa_strerror(int status) {
   }
 }
 
-int fa_version(void) { return 130; }
+int fa_version(void) { return 140; }
 
 }  // extern "C"

@@ -104,13 +104,17 @@ __host__ __device__ __forceinline__ int acc_row(int g, int hh) { return 8 * (g >
 // ===========================================================================
 // dK / dV
 // ===========================================================================
-template <typename E, int D, int BMQ, int BNK>
+// RB: the dQ kernel has already written each query row's -LSE/c and -Delta to
+// Rb ([2, B*H, S]); the tiles then carry those 512 bytes instead of the O tile,
+// and nothing is formed per tile.  Without RB each workgroup forms Delta from the
+// O and dO tiles it stages (every key tile that meets a query tile repeats it).
+template <typename E, int D, int BMQ, int BNK, bool RB>
 __global__ __launch_bounds__(2 * BNK)
 __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, D <= 64 ? 2 : 1)))
 void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
                  const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
-                 uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+                 const float* __restrict__ Rb, uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
                  float* __restrict__ Pk, float* __restrict__ Pv, int nsplit,
                  int B, int H, int Hkv, int S, float scale_log2, float sm_scale) {
   static_assert(BMQ == 64, "a query tile is two 32-row blocks");
@@ -120,7 +124,9 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   constexpr int ROWB = D * 2, CPR = ROWB / 16;
   constexpr int TILE = BMQ * ROWB;                       // bytes of one Q / dO / O tile
   constexpr int NBLK = TILE / 1024;
-  constexpr int BUFA = (3 * TILE + BMQ * 4 + 1023) / 1024 * 1024;  // Q | dO | O | LSE
+  // Q | dO | O | LSE, or with RB: Q | dO | -LSE/c | -Delta
+  constexpr int OFF_L = (RB ? 2 : 3) * TILE;
+  constexpr int BUFA = (OFF_L + (RB ? 2 : 1) * BMQ * 4 + 1023) / 1024 * 1024;
   constexpr int NBUF = 3;
   constexpr int TPR = NT / BMQ;                          // threads per row for Delta
   static_assert(TILE % 1024 == 0, "tiles are whole 1 KB DMA blocks");
@@ -207,18 +213,21 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const int rows = min(BMQ, S - di * BMQ);
     const auto qrs = make_rsrc(Q + row0 * D, rows * ROWB);
     const auto dors = make_rsrc(dO + row0 * D, rows * ROWB);
-    const auto ors = make_rsrc(O + row0 * D, rows * ROWB);
-    const auto lrs = make_rsrc(Lse + row0, rows * 4);
 #pragma unroll
     for (int x = 0; x < NDMA; ++x) {
       const int blk = wave + x * NW;
       if (NBLK % NW == 0 || blk < NBLK) {
         dma16(qrs, buf + blk * 1024, dvo[x], 0);
         dma16(dors, buf + TILE + blk * 1024, dvo[x], 0);
-        dma16(ors, buf + 2 * TILE + blk * 1024, dvo[x], 0);
+        if constexpr (!RB) dma16(make_rsrc(O + row0 * D, rows * ROWB), buf + 2 * TILE + blk * 1024, dvo[x], 0);
       }
     }
-    if (wave == 0) dma4(lrs, buf + 3 * TILE, 4 * lane, 0);
+    if constexpr (RB) {
+      if (wave == 0) dma4(make_rsrc(Rb + row0, rows * 4), buf + OFF_L, 4 * lane, 0);
+      if (wave == 1) dma4(make_rsrc(Rb + (size_t)B * H * S + row0, rows * 4), buf + OFF_L + 4 * BMQ, 4 * lane, 0);
+    } else {
+      if (wave == 0) dma4(make_rsrc(Lse + row0, rows * 4), buf + OFF_L, 4 * lane, 0);
+    }
     if (++dg == G) {
       dg = 0;
       ++di;
@@ -241,6 +250,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // dP - Delta and S - LSE/c directly.
   const float inv_c = 1.0f / scale_log2;
   auto delta_phase = [&](unsigned char* buf, float* dl) __attribute__((always_inline)) {
+    if constexpr (RB) return;
     const int row = tid / TPR, part = tid % TPR;
     float acc = 0.f;
 #pragma unroll
@@ -255,7 +265,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     acc = quad_sum(acc);
     // the four lanes of a row's quad store the same values (no branch, so this
     // joins the surrounding MFMA schedule)
-    float* Ls = reinterpret_cast<float*>(buf + 3 * TILE);
+    float* Ls = reinterpret_cast<float*>(buf + OFF_L);
     const float lsc = -Ls[row] * inv_c;
     dl[row] = -acc;
     Ls[row] = lsc;
@@ -272,7 +282,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       da[x] = lds_read16(buf + TILE, off);
       dob[x] = lds_read16(buf + 2 * TILE, off);
     }
-    ls = reinterpret_cast<const float*>(buf + 3 * TILE)[row];
+    ls = reinterpret_cast<const float*>(buf + OFF_L)[row];
   };
   auto delta_store = [&](unsigned char* buf, float* dl, const u32x4 (&da)[CPR / TPR],
                          const u32x4 (&dob)[CPR / TPR], float ls) __attribute__((always_inline)) {
@@ -284,7 +294,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
       for (int w = 0; w < 4; ++w) acc = dot_pair<E>(da[x][w], dob[x][w], acc);
     acc = quad_sum(acc);
     dl[row] = -acc;
-    reinterpret_cast<float*>(buf + 3 * TILE)[row] = -ls * inv_c;
+    reinterpret_cast<float*>(buf + OFF_L)[row] = -ls * inv_c;
   };
 
   // Accumulator init for query block qb: register g <-> query row 32qb + acc_row(g),
@@ -303,7 +313,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // S - LSE/c = Q_b K^T - LSE/c and dP - Delta = dO_b V^T - Delta for 32-row query
   // block qb: lane (c = key, hh), register g -> query 32 qb + acc_row(g)
   auto sd = [&](const unsigned char* buf, const float* dl, int qb, f32x16& s, f32x16& dp) __attribute__((always_inline)) {
-    s = load_rows(reinterpret_cast<const float*>(buf + 3 * TILE), qb);
+    s = load_rows(reinterpret_cast<const float*>(buf + OFF_L), qb);
     dp = load_rows(dl, qb);
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
@@ -425,7 +435,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     f32x16 s0, dp0, s1, dp1;
     u32x4 pk0[2], dsk0[2], pk1[2], dsk1[2];
     u32x4 ra[2 * KH], rb[2 * KH];
-    const float* lse_s = reinterpret_cast<const float*>(buf + 3 * TILE);
+    const float* lse_s = reinterpret_cast<const float*>(buf + OFF_L);
     s0 = load_rows(lse_s, 0);
     dp0 = load_rows(dl, 0);
     rd_sd(buf, 0, 0, ra);
@@ -456,11 +466,11 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     grad_half(1, s1, dp1, pk1, dsk1);
     u32x4 da[CPR / TPR], dob[CPR / TPR];
     float ls;
-    delta_load(nbuf, da, dob, ls);
+    if constexpr (!RB) delta_load(nbuf, da, dob, ls);
     __builtin_amdgcn_sched_barrier(0);
     rd_w(buf, 1, 1, c_r);
     mm_w(0, ra, pk1, dsk1);
-    delta_store(nbuf, ndl, da, dob, ls);
+    if constexpr (!RB) delta_store(nbuf, ndl, da, dob, ls);
 #pragma unroll
     for (int i1 = 0; i1 < 2; ++i1) {
       c_pk[i1] = pk1[i1];
@@ -487,27 +497,32 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // ---- main loop over the pairs: at the top of iteration t pair t+1 has landed
   // (one barrier makes it and Delta(t) visible), pair t+2 starts its DMA into the
   // buffer pair t-1 used, pair t is computed, Delta(t+1) formed
+  // where pair t's -Delta rows are: formed into delta_s, or staged with the tile
+  auto dlp = [&](int t) __attribute__((always_inline)) -> float* {
+    if constexpr (RB) return reinterpret_cast<float*>(bufp(t) + OFF_L + 4 * BMQ);
+    else return delta_s[t & 1];
+  };
   auto top = [&](int t) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
     if (t + 2 < te) dma_next(bufp(t + 2));
   };
   auto bottom = [&](int t) __attribute__((always_inline)) {
-    if (t + 1 < te) delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
+    if (t + 1 < te) delta_phase(bufp(t + 1), dlp(t + 1));
   };
   if (tb < te) {  // (a chunk of a light key tile can be empty: it stores zeros)
     dma_next(bufp(tb));
     if (tb + 1 < te) dma_next(bufp(tb + 1));
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
-    delta_phase(bufp(tb), delta_s[tb & 1]);
+    delta_phase(bufp(tb), dlp(tb));
   }
   // the pairs on the two tiles that meet this workgroup's keys, then the full tiles
   // (one straight path per loop keeps the accumulators in place across iterations)
   int t = tb;
   for (; t < min(te, TE); ++t) {
     top(t);
-    tile_edge(bufp(t), delta_s[t & 1], (i0 + (t >= G ? 1 : 0)) * BMQ);
+    tile_edge(bufp(t), dlp(t), (i0 + (t >= G ? 1 : 0)) * BMQ);
     bottom(t);
   }
   if (active) {
@@ -516,18 +531,18 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     if constexpr (D == 128) {
       if (t < te) {
         top(t);
-        tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1], BTag<false>{});
+        tile_full_pipelined(bufp(t), dlp(t), bufp(t + 1), dlp(t + 1), BTag<false>{});
         for (++t; t < te; ++t) {
           top(t);
-          tile_full_pipelined(bufp(t), delta_s[t & 1], bufp(t + 1), delta_s[(t + 1) & 1], BTag<true>{});
+          tile_full_pipelined(bufp(t), dlp(t), bufp(t + 1), dlp(t + 1), BTag<true>{});
         }
         mm_w(1, c_r, c_pk, c_dsk);
       }
     } else {
       for (; t < te; ++t) {
         top(t);
-        delta_phase(bufp(t + 1), delta_s[(t + 1) & 1]);
-        tile_full(bufp(t), delta_s[t & 1]);
+        delta_phase(bufp(t + 1), dlp(t + 1));
+        tile_full(bufp(t), dlp(t));
       }
     }
   } else {
@@ -587,7 +602,8 @@ __attribute__((amdgpu_waves_per_eu(dq_waves_per_simd<D, BM, BN>(), dq_waves_per_
 void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                const uint16_t* __restrict__ V, const uint16_t* __restrict__ O,
                const uint16_t* __restrict__ dO, const float* __restrict__ Lse,
-               uint16_t* __restrict__ dQ, int B, int H, int Hkv, int S, float scale_log2, float sm_scale) {
+               uint16_t* __restrict__ dQ, float* __restrict__ Rb, int B, int H, int Hkv, int S,
+               float scale_log2, float sm_scale) {
   constexpr int NW = BM / 32;
   constexpr int NB = BN / 32, KT = D / 16, DB = D / 32;
   constexpr int ROWB = D * 2, CPR = ROWB / 16;
@@ -640,6 +656,12 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     delta = halfwave_sum(part);
   }
   const float lse = Lse[(size_t)bh * S + min(m, S - 1)];
+  // the dK/dV kernel's per-row terms, when it runs after this one: -LSE/c, -Delta
+  if (Rb != nullptr && hh == 0 && m < S) {
+    const float inv_c = 1.0f / scale_log2;
+    Rb[(size_t)bh * S + m] = -lse * inv_c;
+    Rb[(size_t)B * H * S + (size_t)bh * S + m] = -delta;
+  }
 
   TileOffsets<ROWB> to;
   to.init(lane);
@@ -791,11 +813,17 @@ template <typename E, int D, int BMQ, int BNK>
 static bool launch_dkdv(const BwdArgs& a) {
   static_assert(BNK == kDkdvKeys, "host split heuristics assume this key tile");
   const int nsplit = a.nsplit > 1 ? a.nsplit : 1;
-  hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK>), dim3(a.B * a.Hkv * nsplit * ((a.S + BNK - 1) / BNK)),
-                     dim3(2 * BNK), 0, (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
-                     (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
-                     (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv, nsplit, a.B, a.H, a.Hkv, a.S,
-                     a.scale_log2, a.sm_scale);
+  const dim3 grid(a.B * a.Hkv * nsplit * ((a.S + BNK - 1) / BNK)), block(2 * BNK);
+  if (a.rowb)
+    hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK, true>), grid, block, 0, (hipStream_t)a.stream,
+                       (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.o,
+                       (const uint16_t*)a.d_o, a.lse, a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,
+                       nsplit, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
+  else
+    hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK, false>), grid, block, 0, (hipStream_t)a.stream,
+                       (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.o,
+                       (const uint16_t*)a.d_o, a.lse, nullptr, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,
+                       nsplit, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
   if (hipGetLastError() != hipSuccess) return false;
   if (nsplit > 1) {
     const size_t threads = (size_t)a.B * a.Hkv * a.S * (D / 8);
@@ -812,7 +840,7 @@ static bool launch_dq(const BwdArgs& a) {
   hipLaunchKernelGGL((dq_kernel<E, D, BM, BN>), dim3(a.B * a.H * ((a.S + BM - 1) / BM)), dim3(2 * BM), 0,
                      (hipStream_t)a.stream, (const uint16_t*)a.q, (const uint16_t*)a.k,
                      (const uint16_t*)a.v, (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse,
-                     (uint16_t*)a.dq, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
+                     (uint16_t*)a.dq, a.rowb, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
   return hipGetLastError() == hipSuccess;
 }
 
@@ -820,9 +848,17 @@ static bool launch_dq(const BwdArgs& a) {
 // tile.  The dK/dV kernel always runs 4 waves (128 keys) per workgroup over
 // 64-row query tiles: with its K/V rows and two accumulators in registers it
 // holds one wave per SIMD at D = 128, and this shape keeps every SIMD busy and
-// the double-buffered Q/dO/O tiles inside LDS for every head dim.
+// the triple-buffered Q/dO/O tiles inside LDS for every head dim.
+// With a row-terms buffer the dQ kernel runs first and leaves -LSE/c and -Delta
+// of every query row there (it forms Delta once per row, from rows it holds in
+// registers anyway); the dK/dV kernel then stages those instead of the O tiles.
+// Without one, dK/dV runs first and forms Delta from O and dO in every workgroup.
 template <typename E, int D, int BMQ, int BNK>
 static int launch_bwd(const BwdArgs& a) {
+  if (a.rowb) {
+    if (!launch_dq<E, D, BMQ, BNK>(a)) return FA_ERR_LAUNCH;
+    return launch_dkdv<E, D, 64, 128>(a) ? FA_OK : FA_ERR_LAUNCH;
+  }
   if (!launch_dkdv<E, D, 64, 128>(a)) return FA_ERR_LAUNCH;
   return launch_dq<E, D, BMQ, BNK>(a) ? FA_OK : FA_ERR_LAUNCH;
 }

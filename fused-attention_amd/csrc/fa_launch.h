@@ -38,6 +38,9 @@ struct BwdArgs {
   float* wsk;
   float* wsv;
   int nsplit;
+  // [2, B*H, S] fp32: -LSE/c and -Delta of every query row, written by the dQ
+  // kernel (then launched first) for the dK/dV kernel; null: dK/dV forms them
+  float* rowb;
 };
 
 // keys per dK/dV workgroup (4 waves x 32 keys), for the split heuristics on the host

@@ -88,15 +88,22 @@ FA_API int fa_bwd(const void* q, const void* k, const void* v, const void* o,
  * are the sums over its H / H_kv query heads, without atomics.
  *
  * workspace: NULL, or caller-owned device memory of workspace_bytes bytes,
- * 16-byte aligned.  Without it one workgroup per 128-key tile walks every (query
- * tile, query head) pair of the tile and sums them in registers, which leaves most
- * of the GPU idle when B * H_kv * S / 128 is small (MQA, few heads, small batch).
- * With fa_bwd_gqa_workspace_size() bytes each key tile's pairs are split over
- * several workgroups that write fp32 partial sums into the workspace, and a
- * reduction pass on the same stream adds them up (fixed order, deterministic).  A
- * smaller workspace gets the largest split it holds.  The workspace must stay
+ * 16-byte aligned, used in two parts, each only if the rest of the workspace
+ * holds it:
+ *  1. 8 * B * H * S bytes (rounded up to 256): -LSE/c and -Delta of every query
+ *     row.  The dQ kernel then runs first and writes them, and the dK/dV kernel
+ *     reads them instead of forming Delta from the O and dO tiles in each of the
+ *     key tiles that meet a query tile (about 10 % of its time at S = 4096).
+ *  2. fp32 partial dK/dV.  Without them one workgroup per 128-key tile walks every
+ *     (query tile, query head) pair of the tile and sums them in registers, which
+ *     leaves most of the GPU idle when B * H_kv * S / 128 is small (MQA, few heads,
+ *     small batch).  With them each key tile's pairs are split over several
+ *     workgroups that write fp32 partial sums, and a reduction pass on the same
+ *     stream adds them up (fixed order, deterministic); a smaller remainder gets
+ *     the largest split it holds.
+ * fa_bwd_gqa_workspace_size() gives the bytes for both.  The workspace must stay
  * allocated until the stream has passed this call.  H_kv = H (MHA) is accepted:
- * that is how an MHA caller gets the split.
+ * that is how an MHA caller gets either.
  *
  * No counterpart in the reference, whose backward is MHA-only (_check at
  * attention/backward/fused_backward.py:154 rejects K/V of another head count);
@@ -107,9 +114,9 @@ FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o
                int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
                int block_m, int block_n, void* workspace, size_t workspace_bytes, void* hip_stream);
 
-/* Workspace bytes fa_bwd_gqa uses for this shape on the current device (0: none
- * wanted, the key tiles alone fill the GPU; 0 also for invalid dimensions).  No
- * reference counterpart. */
+/* Workspace bytes fa_bwd_gqa uses for this shape on the current device: the
+ * per-row terms, plus the partial sums when the key tiles alone leave the GPU
+ * idle (0 for invalid dimensions).  No reference counterpart. */
 FA_API size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D);
 
 /* 1 if a forward (with_lse 0/1) or backward (is_bwd 1) kernel exists for the

@@ -106,20 +106,25 @@ def test_bwd_gqa_rejects_bad_arguments(lib, kw, code):
     assert bwd_gqa(lib, **kw) == code
 
 
+def rowb(B, H, S):
+    """-LSE/c and -Delta per query row: 8 * B * H * S bytes rounded up to 256."""
+    return (8 * B * H * S + 255) // 256 * 256
+
+
 def test_bwd_gqa_workspace_size(lib):
-    """fp32 partial dK and dV per chunk: 2 * B * H_kv * nsplit * S * D * 4 bytes, with nsplit
-    the chunks per 128-key tile that give 2 x 256 dK/dV workgroups, at most the heaviest key
-    tile's (query tile, query head) pairs and 64."""
+    """The per-row terms, then fp32 partial dK and dV per chunk: 2 * B * H_kv * nsplit * S * D * 4
+    bytes, with nsplit the chunks per 128-key tile that give 2 x 256 dK/dV workgroups, at most the
+    heaviest key tile's (query tile, query head) pairs and 64 (no split below 64 pairs)."""
     ws = lib.fa_bwd_gqa_workspace_size
-    assert ws(2, 32, 32, 4096, 128) == 0                     # 2*32*32 key tiles: no split
-    assert ws(2, 32, 8, 4096, 128) == 0                      # 2*8*32 = 512 workgroups already
-    assert ws(1, 8, 8, 4096, 128) == 2 * 8 * 2 * 4096 * 128 * 4   # MHA, 256 key tiles: 2 chunks
-    assert ws(1, 32, 1, 4096, 64) == 2 * 16 * 4096 * 64 * 4  # MQA: 32 key tiles x 16 chunks
-    assert ws(1, 32, 4, 8192, 128) == 2 * 4 * 2 * 8192 * 128 * 4
-    assert ws(1, 6, 2, 100, 32) == 0                          # 3 heads x 2 query tiles: too short to split
-    assert ws(1, 32, 1, 200, 32) == 2 * 64 * 200 * 32 * 4     # 2 key tiles of 32 x 4 pairs: 64 chunks (the cap)
-    assert ws(2, 8, 8, 2048, 128) == 0                        # 32 pairs per key tile: not worth a split
-    assert ws(1, 1, 1, 64, 64) == 0                           # one pair: nothing to split
+    assert ws(2, 32, 32, 4096, 128) == rowb(2, 32, 4096)              # 2*32*32 key tiles: no split
+    assert ws(2, 32, 8, 4096, 128) == rowb(2, 32, 4096)               # 2*8*32 = 512 workgroups already
+    assert ws(1, 8, 8, 4096, 128) == rowb(1, 8, 4096) + 2 * 8 * 2 * 4096 * 128 * 4  # MHA, 256 key tiles: 2 chunks
+    assert ws(1, 32, 1, 4096, 64) == rowb(1, 32, 4096) + 2 * 16 * 4096 * 64 * 4   # MQA: 32 key tiles x 16 chunks
+    assert ws(1, 32, 4, 8192, 128) == rowb(1, 32, 8192) + 2 * 4 * 2 * 8192 * 128 * 4
+    assert ws(1, 6, 2, 100, 32) == rowb(1, 6, 100)                    # 3 heads x 2 query tiles: too short to split
+    assert ws(1, 32, 1, 200, 32) == rowb(1, 32, 200) + 2 * 64 * 200 * 32 * 4  # 2 key tiles of 32 x 4 pairs: 64 chunks (the cap)
+    assert ws(2, 8, 8, 2048, 128) == rowb(2, 8, 2048)                 # 32 pairs per key tile: not worth a split
+    assert ws(1, 1, 1, 64, 64) == rowb(1, 1, 64)                      # one pair: nothing to split
     for bad in ((0, 4, 2, 256, 64), (1, 4, 3, 256, 64), (1, 4, 2, 0, 64), (1, 4, 2, 256, 48)):
         assert ws(*bad) == 0
 

@@ -160,3 +160,40 @@ def test_backward_partial_key_tile(N, D):
     """S not a multiple of the dK/dV kernel's 128-key workgroup: its upper waves idle."""
     q, k, v, do = inputs((1, 2, N, D), seed=N + D, dtype=torch.bfloat16)
     check_grads(q, k, v, do, (64, 64), f"bwd partial N{N} D{D}")
+
+
+def _fa_bwd_no_workspace(q, k, v, do, tiles):
+    """dQ, dK, dV from the reference-compatible entry point fa_bwd: no workspace, dK/dV first,
+    Delta formed inside both kernels (the Python layer takes fa_bwd_gqa with a workspace)."""
+    import ctypes
+    import math
+    from attention import _lib
+    from attention.backward.fused_backward import _forward
+    B, H, S, D = q.shape
+    o, lse = _forward(q, k, v, *tiles)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    code = _lib.load().fa_bwd(*(ctypes.c_void_p(t.data_ptr()) for t in (q, k, v, o, do, lse, dq, dk, dv)),
+                              B, H, S, D, _lib.dtype_code(q.dtype), _lib.scale_log2(D), 1.0 / math.sqrt(D),
+                              tiles[0], tiles[1], _lib._stream(q.device))
+    _lib.check(code, "fa_bwd")
+    torch.cuda.synchronize()
+    return dq, dk, dv
+
+
+@pytest.mark.parametrize("shape,dt,tiles", [((1, 3, 300, 32), "fp16", (64, 64)), ((2, 2, 257, 64), "bf16", (128, 64)),
+                                            ((1, 4, 1000, 128), "bf16", (128, 64)), ((1, 2, 640, 128), "fp16", (64, 128)),
+                                            ((4, 32, 4096, 128), "bf16", (128, 64))],
+                         ids=lambda x: "x".join(map(str, x)) if isinstance(x, tuple) else x)
+def test_reference_entry_without_workspace(shape, dt, tiles):
+    """fa_bwd (dK/dV then dQ, Delta formed in both) against the fp32 reference at the max-abs bar,
+    and against the Python path (dQ first, dK/dV reading the per-row terms): dQ bitwise equal,
+    dK/dV equal up to the fp32 summation order of Delta."""
+    q, k, v, do = inputs(shape, seed=sum(shape), dtype=DTYPES[dt])
+    log(f"fa_bwd without workspace {shape} {dt} {tiles}")
+    got = _fa_bwd_no_workspace(q, k, v, do, tiles)
+    py = run_fused(q, k, v, do, tiles)[1:]
+    assert torch.equal(got[0], py[0])
+    ref = reference_grads(q, k, v, do)[1:]
+    for name, g, p, r in zip(("dQ", "dK", "dV"), got, py, ref):
+        assert float((g.float() - r).abs().max()) <= MAX_ABS, name
+        assert float((g.float() - p.float()).abs().max()) <= 1e-2 + 1e-2 * float(r.abs().max()), name
