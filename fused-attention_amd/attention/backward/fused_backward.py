@@ -7,13 +7,16 @@ Forward  = the fused forward kernel with the LSE output switched on: it writes
            log2(e)/sqrt(D)) directly, where the reference stores m and l and adds
            them with a torch op (:61-62, :169).
 Backward = two atomic-free kernels on the same stream:
-  dK/dV kernel: one workgroup per key tile; loops over the query tiles that see it,
-                recomputing P from the LSE; dV = P^T dO, dK = scale * dS^T Q.
   dQ kernel:    one workgroup per query tile; loops over the visible key tiles;
-                dQ = scale * dS K.
-  with dS = P * (dP - Delta), dP = dO V^T and Delta = rowsum(dO * O) computed
-  inside both kernels from the O and dO rows they already read (the reference
-  runs it as a separate torch op, :175).
+                dQ = scale * dS K.  Forms Delta = rowsum(dO * O) from the O and dO
+                rows it holds in registers (the reference runs it as a separate torch
+                op, :175) and leaves each row's -LSE/c and -Delta in a small workspace.
+  dK/dV kernel: one workgroup per key tile; loops over the query tiles that see it,
+                recomputing P from the LSE; dV = P^T dO, dK = scale * dS^T Q, reading
+                the per-row terms instead of forming Delta in every key tile.
+  with dS = P * (dP - Delta) and dP = dO V^T.  (The C entry fa_bwd keeps the
+  reference's order, dK/dV then dQ, with Delta formed in both kernels and no
+  workspace; the results differ only in Delta's fp32 summation order.)
 
 Shapes: q, k, v are (B, H, N, D) float16 or bfloat16, any N (a partial last tile
 is masked), tiles 64 or 128.

@@ -4,12 +4,15 @@
 //   P  = exp2(S*c - LSE)     with S = Q K^T, c = log2(e)/sqrt(D), LSE from the forward
 //   dV = P^T dO              dP = dO V^T        Delta = rowsum(dO * O)
 //   dS = P * (dP - Delta)    dQ = dS K / sqrt(D)  dK = dS^T Q / sqrt(D)
-// Two kernels, launched in this order on the caller's stream:
+// Two kernels on the caller's stream: dK/dV then dQ, each forming Delta itself;
+// or, given a buffer for per-row terms, dQ first (it writes each query row's
+// -LSE/c and -Delta) and then dK/dV, which reads them instead of forming Delta.
 //   dkdv_kernel: one workgroup per key tile (128 keys, 32 per wave) of one K/V
 //                head; walks the (64-row query tile, query head) pairs at and below
 //                the diagonal (G = H / Hkv heads per K/V head; 1 for MHA).  Per pair,
-//                Q, dO, O and LSE are copied global -> LDS by DMA (triple buffered)
-//                and Delta is formed from the O and dO tiles in LDS.  Each wave keeps
+//                Q, dO, O and LSE (or Q, dO and the per-row terms) are copied
+//                global -> LDS by DMA (triple buffered), and Delta is formed from
+//                the O and dO tiles in LDS when not handed over.  Each wave keeps
 //                its K and V rows in registers as MFMA B operands, computes S = Q K^T
 //                and dP = dO V^T with one lane per key, and accumulates
 //                dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and Q^T with
@@ -23,7 +26,8 @@
 //                the key tiles (tile_n keys) up to the diagonal, heavy first.  Each
 //                wave keeps Q and dO rows in registers, computes S^T = K Q^T and
 //                dP^T = V dO^T with one lane per query (LSE and Delta are per-lane
-//                scalars; Delta comes from the O and dO rows in the prologue) and
+//                scalars; Delta comes from the O and dO rows in the prologue, and is
+//                stored with -LSE/c as the per-row terms when dK/dV runs after) and
 //                accumulates dQ^T += K^T dS^T, reading K^T with transposed reads.
 // No kernel uses atomics; each output element is written once.  Any S >= 1: the
 // last query and key tiles may be partial (rows past S read as zero, never stored).
