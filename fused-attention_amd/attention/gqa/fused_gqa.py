@@ -7,8 +7,10 @@ K/V head h // (H // H_kv).  One workgroup serves up to four query heads of the
 same K/V group, so each K/V tile staged in LDS is reused across those heads.
 
 Beyond the reference (whose backward is MHA-only): the same attention with
-autograd, whose backward runs dK/dV (one workgroup per K/V-head key tile, summing
-the group's query heads in registers, no atomics) then dQ:
+autograd, whose backward runs dQ (which also leaves each row's Delta and LSE term
+for the next kernel) then dK/dV (one workgroup per K/V-head key tile, summing the
+group's query heads in registers, no atomics; split over several workgroups with
+fp32 partial sums when the key tiles alone leave the GPU idle):
 
     O = fused_gqa_attention_autograd(q, k, v, tile_m=64, tile_n=64); O.backward(dO)
 """
