@@ -55,6 +55,18 @@ struct BTag {
   static constexpr bool value = B;
 };
 
+template <int I>
+using IC = std::integral_constant<int, I>;
+
+// f(IC<I>{}) for I = I0 .. N-1, each with its index as a compile-time constant
+template <int I0, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I0 < N) {
+    f(IC<I0>{});
+    static_for<I0 + 1, N>(f);
+  }
+}
+
 // Chunk swizzle of row r for rows of cpr 16-byte chunks (cpr = 16, 8 or 4: rows
 // of 256, 128 or 64 bytes, i.e. 1, 2 or 4 rows per bank line).
 __host__ __device__ __forceinline__ int bswz(int r, int cpr) {
@@ -744,6 +756,91 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
   };
 
+  // Full tiles at D = 128 with 64-key tiles, pipelined by hand.  Left to itself the
+  // compiler issues each MFMA's LDS operand read just before it and waits for it
+  // (one read in flight).  Here a tile is a sequence of items, NB blocks of 32 keys
+  // each made of KT/2 S/dP items (two k-steps: 2 S and 2 dP MFMAs) and DB/2 dQ
+  // items (two d blocks x two key halves: 4 MFMAs), each item with 4 operands.
+  // Item m's operands are read in the region of item m-2's MFMAs (three rotating
+  // buffers, regions pinned by sched_barrier); P and dS of a block run in a region
+  // of their own after its last S/dP item; a tile's last item runs at the start of
+  // the next tile, under the operand reads that follow the barrier.  Same
+  // arithmetic in the same order as compute() (bitwise equal).
+  constexpr bool PIPE = (D == 128 && BN == 64);
+  constexpr int IK = KT / 2, IB = IK + DB / 2, NITEM = NB * IB;
+  u32x4 pb[3][4];
+  u32x4 dsk_c[2];      // dS of the current block, kept for the deferred item
+  f32x16 s_c, dp_c;
+  auto rd_item = [&](const unsigned char* Ks, auto mt) __attribute__((always_inline)) {
+    constexpr int m = decltype(mt)::value, nb = m / IB, k = m % IB, bi = m % 3;
+    if constexpr (k < IK) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int o = to.opnd[2 * k + x] + 32 * nb * ROWB;
+        pb[bi][2 * x] = lds_read16(Ks, o);
+        pb[bi][2 * x + 1] = lds_read16(Ks + TILE, o);
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const int db = 2 * (k - IK) + jj, u = 2 * nb + i1;
+          pb[bi][2 * jj + i1] = tr_read2(Ks, to.tr(db, u, 0), to.tr(db, u, 1));
+        }
+    }
+  };
+  auto mm_item = [&](auto mt) __attribute__((always_inline)) {
+    constexpr int m = decltype(mt)::value, k = m % IB, bi = m % 3;
+    if constexpr (k < IK) {
+      if constexpr (k == 0) {
+        s_c = f32x16{};
+        dp_c = f32x16{};
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        s_c = mfma32<E>(pb[bi][2 * x], qf[2 * k + x], s_c);
+        dp_c = mfma32<E>(pb[bi][2 * x + 1], dof[2 * k + x], dp_c);
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const int db = 2 * (k - IK) + jj;
+          acc[db] = mfma32<E>(pb[bi][2 * jj + i1], dsk_c[i1], acc[db]);
+        }
+    }
+  };
+  auto grad_block = [&]() __attribute__((always_inline)) {
+    float ds[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const float p = fast_exp2(__builtin_fmaf(s_c[g], scale_log2, -lse));
+      ds[g] = p * (dp_c[g] - delta);
+    }
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dsk_c[i1][q] = pack2<E>(ds[8 * i1 + 2 * q], ds[8 * i1 + 2 * q + 1]);
+  };
+  auto tile_pipelined = [&](const unsigned char* Ks, auto prev) __attribute__((always_inline)) {
+    rd_item(Ks, IC<0>{});
+    rd_item(Ks, IC<1>{});
+    if constexpr (decltype(prev)::value) mm_item(IC<NITEM - 1>{});   // the previous tile's last item
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NITEM - 1>([&](auto mt) __attribute__((always_inline)) {
+      constexpr int m = decltype(mt)::value;
+      if constexpr (m + 2 < NITEM) rd_item(Ks, IC<m + 2>{});
+      mm_item(mt);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (m % IB == IK - 1) {   // the block's S and dP are complete
+        grad_block();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
+  };
+
   auto step = [&](int j, auto par_tag, auto mask_tag) __attribute__((always_inline)) {
     constexpr bool P = decltype(par_tag)::value;
     unsigned char* cur = P ? lds1 : lds0;
@@ -753,18 +850,42 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
   };
+  auto step_pipelined = [&](int j, auto par_tag, auto prev) __attribute__((always_inline)) {
+    constexpr bool P = decltype(par_tag)::value;
+    unsigned char* cur = P ? lds1 : lds0;
+    unsigned char* nxt = P ? lds0 : lds1;
+    if (j + 1 < ntiles) dma_tile(j + 1, nxt);
+    tile_pipelined(cur, prev);
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+  };
 
   dma_tile(0, lds0);
   __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
   __syncthreads();
   int j = 0;
-  for (; j + 1 < jfull; j += 2) {
-    step(j, BTag<false>{}, BTag<false>{});
-    step(j + 1, BTag<true>{}, BTag<false>{});
-  }
-  if (j < jfull) {
-    step(j, BTag<false>{}, BTag<false>{});
-    ++j;
+  if constexpr (PIPE) {
+    if (jfull > 0) {
+      step_pipelined(0, BTag<false>{}, BTag<false>{});
+      for (j = 1; j + 1 < jfull; j += 2) {
+        step_pipelined(j, BTag<true>{}, BTag<true>{});
+        step_pipelined(j + 1, BTag<false>{}, BTag<true>{});
+      }
+      if (j < jfull) {
+        step_pipelined(j, BTag<true>{}, BTag<true>{});
+        ++j;
+      }
+      mm_item(IC<NITEM - 1>{});   // the last full tile's last item
+    }
+  } else {
+    for (; j + 1 < jfull; j += 2) {
+      step(j, BTag<false>{}, BTag<false>{});
+      step(j + 1, BTag<true>{}, BTag<false>{});
+    }
+    if (j < jfull) {
+      step(j, BTag<false>{}, BTag<false>{});
+      ++j;
+    }
   }
   for (; j < ntiles; ++j) {
     if (j & 1) step(j, BTag<true>{}, BTag<true>{});
