@@ -263,7 +263,8 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // Per tile, once: -Delta into dl (TPR threads per row, chunk subsets, shuffles)
   // and the tile's LSE slice rewritten in place as -LSE / c.  Both are then the
   // initial accumulators of the dP and S products, so the MFMAs deliver
-  // dP - Delta and S - LSE/c directly.
+  // dP - Delta and S - LSE/c directly.  With RB both arrive staged with the tile
+  // and there is nothing to form.
   const float inv_c = 1.0f / scale_log2;
   auto delta_phase = [&](unsigned char* buf, float* dl) __attribute__((always_inline)) {
     if constexpr (RB) return;
