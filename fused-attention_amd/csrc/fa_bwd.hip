@@ -29,6 +29,8 @@
 //                scalars; Delta comes from the O and dO rows in the prologue, and is
 //                stored with -LSE/c as the per-row terms when dK/dV runs after) and
 //                accumulates dQ^T += K^T dS^T, reading K^T with transposed reads.
+//                At D >= 64 the full tiles run a hand-pipelined schedule (operand
+//                reads two items ahead of their MFMAs).
 // No kernel uses atomics; each output element is written once.  Any S >= 1: the
 // last query and key tiles may be partial (rows past S read as zero, never stored).
 //
@@ -757,7 +759,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
   };
 
-  // Full tiles at D = 128 with 64-key tiles, pipelined by hand.  Left to itself the
+  // Full tiles at D >= 64, pipelined by hand.  Left to itself the
   // compiler issues each MFMA's LDS operand read just before it and waits for it
   // (one read in flight).  Here a tile is a sequence of items, NB blocks of 32 keys
   // each made of KT/2 S/dP items (two k-steps: 2 S and 2 dP MFMAs) and DB/2 dQ
@@ -767,7 +769,7 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // of their own after its last S/dP item; a tile's last item runs at the start of
   // the next tile, under the operand reads that follow the barrier.  Same
   // arithmetic in the same order as compute() (bitwise equal).
-  constexpr bool PIPE = (D == 128 && BN == 64);
+  constexpr bool PIPE = (D >= 64);
   constexpr int IK = KT / 2, IB = IK + DB / 2, NITEM = NB * IB;
   u32x4 pb[3][4];
   u32x4 dsk_c[2];      // dS of the current block, kept for the deferred item
