@@ -16,7 +16,7 @@
 //                its K and V rows in registers as MFMA B operands, computes S = Q K^T
 //                and dP = dO V^T with one lane per key, and accumulates
 //                dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and Q^T with
-//                ds_read_b64_tr_b16.  At D = 128 the full tiles run a hand-pipelined
+//                ds_read_b64_tr_b16.  At D >= 64 the full tiles run a hand-pipelined
 //                schedule (operand reads a region ahead of their MFMAs).
 //   dkdv_reduce_kernel: only with a caller workspace, when B * H_kv key tiles alone
 //                would leave the GPU idle (MQA, few heads): each key tile's pairs are
@@ -386,15 +386,15 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     wacc(buf, 1, pk1, dsk1);
   };
 
-  // The same tile at D = 128 (one wave per SIMD, so nothing else hides its LDS
-  // latency), as seven regions pinned by sched_barrier: each issues the operand
-  // reads of the next region's 8 MFMAs while its own 8 run, the P / dS math is spread
+  // The same tile at D >= 64, as seven regions pinned by sched_barrier (at D = 128
+  // one wave per SIMD, so nothing else hides its LDS latency; at D = 64 two): each
+  // issues the operand reads of the next region's MFMAs while its own run, the P / dS math is spread
   // over four of them in halves, the reads of the next tile's Delta go out a region
   // before its arithmetic, and the last 8 dV/dK MFMAs (block 1, second half) move to
   // the first region of the next tile, where they cover the reads that follow its
   // barrier.  Same arithmetic in the same order as tile_full (bitwise equal); 12 %
-  // faster at the headline shape than the compiler's own schedule, whose MFMAs each
-  // waited for an operand read issued just before them.
+  // faster at D = 128 (B=4 H=32 S=4096) than the compiler's own schedule, whose MFMAs
+  // each waited for an operand read issued just before them, 3 % at D = 64.
   constexpr int KH = KT / 2, DH = DB / 2;
   auto rd_sd = [&](const unsigned char* buf, int qb, int half, u32x4 (&r)[2 * KH]) __attribute__((always_inline)) {
 #pragma unroll
@@ -547,7 +547,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   if (active) {
     // Delta(t+1) is formed first, in the same schedule as pair t's MFMAs; after
     // the last pair it runs on the idle buffer and its result is never read
-    if constexpr (D == 128) {
+    if constexpr (D >= 64) {
       if (t < te) {
         top(t);
         tile_full_pipelined(bufp(t), dlp(t), bufp(t + 1), dlp(t + 1), BTag<false>{});
