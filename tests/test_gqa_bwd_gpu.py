@@ -179,6 +179,8 @@ def test_dkdv_split_matches_register_sums(shape):
     assert all(torch.equal(a, b) for a, b in zip(got, again))
     half = _bwd_through_abi(q, k, v, o, do, lse, need // 2)
     rows_only = _bwd_through_abi(q, k, v, o, do, lse, rows)  # dQ first, no split
+    too_small = _bwd_through_abi(q, k, v, o, do, lse, rows - 256)  # holds neither part: as NULL
+    assert all(torch.equal(a, b) for a, b in zip(too_small, ref))
     for out in (half, rows_only):
         assert torch.equal(out[0], ref[0])
         for g, r in zip(out[1:], ref[1:]):
