@@ -66,14 +66,11 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
   return FA_OK;
 }
 
-// Workgroups the dK/dV kernel should have for its heavy-first order to balance:
-// two rounds of one workgroup per CU (a split costs an fp32 partial write, read
-// and reduction, so it is kept to what load balance needs).  The CU count is
-// read once per device: the workspace query and the launch both ask on every
-// backward, and a short backward is bound by host time.
+// CU count of the current device, read once per device: the launch paths ask on
+// every call, and a short call is bound by host time.
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cus[kMaxDevices];
-int dkdv_target_workgroups() {
+int cu_count() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   int cus = (dev >= 0 && dev < kMaxDevices) ? g_cus[dev].load(std::memory_order_relaxed) : 0;
@@ -84,8 +81,25 @@ int dkdv_target_workgroups() {
     else if (dev < kMaxDevices)
       g_cus[dev].store(cus, std::memory_order_relaxed);
   }
-  return 2 * cus;
+  return cus;
 }
+
+// Forward query heads per workgroup for this launch: heads_per_wg's choice, but
+// four heads (64-row tiles) drop to two when the grid would hold fewer than four
+// workgroups per CU, where the heavy-first order cannot balance the causal
+// triangle (B=2 H=8 H_kv=1 S=8192 fp16, tile 64x64: D=128 0.328 -> 0.288 ms,
+// D=32 0.175 -> 0.123 ms; at B=2 H=32 H_kv=8, 2048 workgroups, four stay 3 %
+// faster).  Two heads of 64 rows still hold two waves per SIMD.
+int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
+  int gh = heads_per_wg(group, block_m, block_n);
+  if (gh == 4 && (long long)B * (H / 4) * ((S + block_m - 1) / block_m) < 4LL * cu_count()) gh = 2;
+  return gh;
+}
+
+// Workgroups the dK/dV kernel should have for its heavy-first order to balance:
+// two rounds of one workgroup per CU (a split costs an fp32 partial write, read
+// and reduction, so it is kept to what load balance needs).
+int dkdv_target_workgroups() { return 2 * cu_count(); }
 
 size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
   return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
@@ -128,7 +142,7 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   if (st != FA_OK) return st;
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o) return FA_ERR_NULL;
-  const int gh = heads_per_wg(H / H_kv, block_m, block_n);
+  const int gh = fwd_heads_per_wg(B, H, H / H_kv, S, block_m, block_n);
   fa::FwdFn fn = fwd_table(dtype, D, block_m, block_n, gh, lse != nullptr);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::FwdArgs a{q, k, v, o, lse, B, H, H_kv, S, D, scale_log2, hip_stream};

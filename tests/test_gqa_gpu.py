@@ -70,3 +70,19 @@ def test_gqa_equals_mha_on_repeated_kv(group):
     b = fused_attention(q, k.repeat_interleave(group, 1).contiguous(), v.repeat_interleave(group, 1).contiguous(), 64, 64)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [32, 128])
+def test_heads_per_workgroup_do_not_change_results(D):
+    """With 64-row tiles a workgroup serves four heads of a K/V group when the grid is large
+    (B=1 H=32 H_kv=4 S=8192: 1024 workgroups) and two when it is small (the same heads 0..7
+    alone: 256 workgroups).  Each row's arithmetic is the same either way: bitwise equal."""
+    g = torch.Generator(device="cuda").manual_seed(D)
+    q = torch.randn(1, 32, 8192, D, device="cuda", generator=g).half()
+    k, v = (torch.randn(1, 4, 8192, D, device="cuda", generator=g).half() for _ in range(2))
+    log(f"gqa heads-per-workgroup B1 H32 Hkv4 S8192 D{D}")
+    big = fused_gqa_attention(q, k, v, 64, 64)
+    small = fused_gqa_attention(q[:, :8].contiguous(), k[:, :1].contiguous(), v[:, :1].contiguous(), 64, 64)
+    torch.cuda.synchronize()
+    assert torch.isfinite(big).all()
+    assert torch.equal(big[:, :8], small)
