@@ -96,6 +96,19 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
   return gh;
 }
 
+// tile_m only sets how many 32-row waves share a workgroup: each 32-row group runs
+// the same arithmetic over the same key tiles either way, so results do not depend
+// on it (bitwise).  A single-head workgroup of 64 rows holds two waves, and with
+// its K and V tiles double-buffered in LDS it gets one wave per SIMD
+// or less; where that is measured slower, tile_m = 64 runs as 128-row workgroups.
+// Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows: tile_n = 64:
+// D=128 685 -> 970, D=64 582 -> 809, D=32 358 -> 552; tile_n = 128: D=128 350 -> 637
+// (D <= 64 about equal, so left).  dQ: D = 128 only (both tile_n).
+int fwd_block_m(int block_m, int block_n, int D, int gh) {
+  return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
+}
+int dq_block_m(int block_m, int D) { return (block_m == 64 && D == 128) ? 128 : block_m; }
+
 // Workgroups the dK/dV kernel should have for its heavy-first order to balance:
 // two rounds of one workgroup per CU (a split costs an fp32 partial write, read
 // and reduction, so it is kept to what load balance needs).
@@ -143,7 +156,7 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o) return FA_ERR_NULL;
   const int gh = fwd_heads_per_wg(B, H, H / H_kv, S, block_m, block_n);
-  fa::FwdFn fn = fwd_table(dtype, D, block_m, block_n, gh, lse != nullptr);
+  fa::FwdFn fn = fwd_table(dtype, D, fwd_block_m(block_m, block_n, D, gh), block_n, gh, lse != nullptr);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::FwdArgs a{q, k, v, o, lse, B, H, H_kv, S, D, scale_log2, hip_stream};
   return fn(a);
@@ -156,7 +169,7 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
   int st = check_common(B, H, S, D, dtype, block_m, block_n);
   if (st != FA_OK) return st;
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
-  fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
+  fa::BwdFn fn = bwd_table(dtype, D, dq_block_m(block_m, D), block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream,
                 nullptr, nullptr, 1, nullptr};
@@ -178,7 +191,7 @@ int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15)) return FA_ERR_WORKSPACE;
-  fa::BwdFn fn = bwd_table(dtype, D, block_m, block_n);
+  fa::BwdFn fn = bwd_table(dtype, D, dq_block_m(block_m, D), block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
   // the workspace holds, in this order and as far as it reaches: the per-row terms
   // (dQ then runs first and dK/dV reads Delta instead of forming it), then the

@@ -116,3 +116,23 @@ def test_non_default_stream_and_repeatability():
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("tn", [64, 128])
+def test_tile_m_does_not_change_results(D, tn):
+    """tile_m sets how many 32-row waves share a workgroup; every 32-row group runs the same
+    arithmetic over the same key tiles either way, so O, LSE, dQ, dK and dV of tile_m = 64 and
+    tile_m = 128 are bitwise equal (partial tiles included)."""
+    from attention.backward.fused_backward import _backward, _forward
+    g = torch.Generator(device="cuda").manual_seed(D + tn)
+    q, k, v, do = (torch.randn(1, 4, 1000, D, device="cuda", generator=g).bfloat16() for _ in range(4))
+    log(f"tile_m invariance D{D} tile_n {tn}")
+    o64, l64 = _forward(q, k, v, 64, tn)
+    o128, l128 = _forward(q, k, v, 128, tn)
+    torch.cuda.synchronize()
+    assert torch.equal(o64, o128) and torch.equal(l64, l128)
+    g64 = _backward(q, k, v, o64, l64, do, 64, tn)
+    g128 = _backward(q, k, v, o128, l128, do, 128, tn)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(g64, g128))
