@@ -55,6 +55,9 @@ enum fa_status {
  * scale_log2 : log2(e) / sqrt(D) as the reference folds it (fused.py:74).
  * Query head h reads K/V head h / (H / H_kv) (fused_gqa.py:18).
  * block_m / block_n : query rows per head and keys per LDS tile, each in {64, 128}.
+ *        block_m cannot change the result (each 32-row wave computes the same
+ *        either way); where a 64-row single-head workgroup would leave SIMDs idle
+ *        the library runs 128-row workgroups.
  *        S may be any length >= 1: a partial last query or key tile is masked (the
  *        reference requires S to be a multiple of both tiles, fused.py:70-71, and
  *        names partial edge tiles as future work).
