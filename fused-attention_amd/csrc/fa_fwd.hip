@@ -333,7 +333,7 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   constexpr int NPV = DB * 2 * NB;
   u32x4 pvb[3];
   auto pv_read = [&](const unsigned char* Vs, int i) __attribute__((always_inline)) {
-    const int db = i / (2 * NB), u = i % (2 * NB);
+    const int db = i % DB, u = i / DB;
     const int o = ((db & 1) ? voff_odd : voff_even) + 64 * db + 16 * u * ROWB;
     return lds_read_tr16x2(Vs, o, o + 8 * ROWB);
   };
@@ -345,7 +345,7 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 #pragma unroll
     for (int i = 0; i < NPV; ++i) {
       if (i + 2 < NPV) pvb[(i + 2) % 3] = pv_read(Vs, i + 2);
-      acc[i / (2 * NB)] = mfma32<E>(pvb[i % 3], pk[i % (2 * NB)], acc[i / (2 * NB)]);
+      acc[i % DB] = mfma32<E>(pvb[i % 3], pk[i / DB], acc[i % DB]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
