@@ -322,14 +322,11 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     }
   };
 
-  // ---- software pipeline over key tiles.  Iteration j: wait for K(j+1) and
-  // V(j), start the DMA of K(j+2) and V(j+1), then S(j+1) on the MFMA pipe
-  // while the VALU turns S(j) into P(j), then PV(j).  K runs one tile ahead of
-  // V; both are double-buffered.
   // PV of a full tile with its V^T operands read two MFMAs ahead (three rotating
-  // buffers, pinned by sched_barrier), the first two before the softmax.  Left to
-  // itself the compiler read one operand ahead and waited on it before every
-  // MFMA; same MFMAs in the same order as pv() (bitwise equal), 2 % faster.
+  // buffers, pinned by sched_barrier), the first two before the softmax, and the
+  // four d blocks' accumulators taking turns.  Left to itself the compiler read
+  // one operand ahead and waited on it before every MFMA.  Each accumulator sees
+  // the same MFMAs in the same order as in pv() (bitwise equal); 2 % faster.
   constexpr int NPV = DB * 2 * NB;
   u32x4 pvb[3];
   auto pv_read = [&](const unsigned char* Vs, int i) __attribute__((always_inline)) {
@@ -352,8 +349,12 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   auto Kbuf = [&](int j) __attribute__((always_inline)) { return lds + (j & 1) * TILE; };
   auto Vbuf = [&](int j) __attribute__((always_inline)) { return lds + 2 * TILE + (j & 1) * TILE; };
 
-  // (one scope with restrict-qualified buffers: the tiles read are never the DMA
-  // targets, so the compiler need not wait for the DMA before the transposed reads)
+  // ---- software pipeline over key tiles.  Iteration j: wait for K(j+1) and
+  // V(j), start the DMA of K(j+2) and V(j+1), then S(j+1) on the MFMA pipe
+  // while the VALU turns S(j) into P(j), then PV(j).  K runs one tile ahead of
+  // V; both are double-buffered.  (The body is one scope with restrict-qualified
+  // buffers: the tiles read are never the DMA targets, so the compiler need not
+  // wait for the DMA before the transposed reads.)
   auto body = [&](int j, const unsigned char* __restrict__ kcur, unsigned char* __restrict__ kdst,
                   const unsigned char* __restrict__ vcur, unsigned char* __restrict__ vdst,
                   f32x16 (&sc)[NB], int nvc, f32x16 (&sn)[NB], int& nvn, auto mt) __attribute__((always_inline)) {
