@@ -1,0 +1,418 @@
+// fa_fwd.hip - causal attention forward for gfx950 (MHA, GQA/MQA, optional LSE).
+//
+// Algorithm (the reference's online softmax, attention/fused/fused.py:11-65,
+// attention/gqa/fused_gqa.py:12-67, attention/backward/fused_backward.py:26-62):
+//   per query row: m = -inf, l = 0, acc = 0 (fp32)
+//   for every key tile j up to the diagonal:
+//     s = q . k                     (fp32 MFMA accumulation)
+//     s = -inf where key > query    (only on tiles that straddle the diagonal)
+//     m_new = max(m, rowmax(s) * c) with c = log2(e)/sqrt(D)
+//     alpha = exp2(m - m_new); p = exp2(s*c - m_new)
+//     P = p rounded to the input type
+//     l = l*alpha + rowsum(P)
+//     acc = acc*alpha + P . v
+//   O = acc / l; optional LSE = m + log2(l) (fused_backward.py:169).
+// Two differences from the reference's arithmetic, both far inside the fp32
+// reference's tolerance: l sums the rounded P that the PV product uses (the
+// reference sums the unrounded p, fused.py:59), so O is an exactly normalised
+// average of the V rows it weights; and the reference point m is lazy: a tile's
+// p is computed against the current m, and only if some lane's sum of p over
+// the tile exceeds 2^FA_RESCALE_THRESHOLD (or is not finite) is the tile's row
+// max taken, acc and l rescaled and p recomputed.  Every p therefore stays
+// <= 2^T, no row max is reduced on the common path, and O = acc / l and
+// LSE = m + log2(l) do not depend on the reference point; because l sums the
+// same rounded weights as acc, a row dominated by one key still reproduces
+// that key's V row exactly.
+//
+// MI355X mapping:
+//   * one workgroup = GH query heads (sharing one K/V head) x BM query rows;
+//     one wave = one head x 32 query rows; WR = BM/32 waves per head.
+//   * each wave computes S^T = K Q^T (keys x queries) so a lane owns ONE query
+//     row: row max / row sum are register-local plus one permlane32 swap, and the
+//     score accumulator is fed straight back as the B operand of O^T += V^T P^T.
+//   * Q stays in registers for the whole loop.  K and V tiles go global -> LDS
+//     with buffer_load_dwordx4 ... lds (no VGPR staging; the per-lane source
+//     offsets are fixed, the tile offset is a scalar), double-buffered in two
+//     LDS arrays; the next tile's DMA runs while the current tile is computed.
+//   * V^T operands come from ds_read_b64_tr_b16 on the row-major V tile, so no
+//     transpose is ever materialised.
+//   * causal skipping at two levels: key tiles past the workgroup's last row are
+//     never loaded, and each wave skips 32-key blocks past its own last row;
+//     tiles wholly below the diagonal run a mask-free path.
+//   * heavy-first, XCD-aware order: the 8 XCDs each take a contiguous range of
+//     (batch, head-group) units; inside a unit the last (heaviest) query tile
+//     is dispatched first.
+//
+// LDS layouts (one buffer = K tile then V tile, each BN rows x D, row-major).
+// gfx950's LDS has 64 banks of 4 bytes: a 16-byte read is served 16 lanes per
+// cycle and an 8-byte read 16 lanes per cycle (measured: 16-byte reads stream at
+// twice the bytes per clock of 8-byte reads), so a read is conflict free when
+// the lanes of each 16-lane phase touch distinct banks.
+//   K: 16-byte chunk ch of row r stored at chunk ch ^ kswz(r), kswz(r) =
+//      (r * CPR / 16) & (CPR - 1) with CPR chunks per row; an MFMA A-operand
+//      read (lane c reads row c, one chunk) then puts the 16 lanes of a phase
+//      on 16 distinct 16-byte bank slots.
+//   V: byte b of row r stored at b ^ (32 * (r & 3)); a transposed read (16 lanes
+//      = 4 rows x 32 bytes) then hits 4 distinct 32-byte bank groups.
+#include "fa_device.h"
+#include "fa_launch.h"
+
+namespace fa {
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+constexpr int kWaitVmcnt0 = 0x0F70;
+// p is recomputed against a fresh row max only when a lane's sum of p over a
+// tile exceeds 2^FA_RESCALE_THRESHOLD
+#ifndef FA_RESCALE_THRESHOLD
+#define FA_RESCALE_THRESHOLD 8
+#endif
+constexpr float kSumLimit = float(1 << FA_RESCALE_THRESHOLD);
+
+template <int D, int BM, int BN, int GH>
+constexpr int fwd_waves_per_simd() {
+  return (BN == 64 && (BM / 32) * GH >= 4) ? 2 : 1;
+}
+
+// Compile-time "tile is below the diagonal" marker, and its run-time twin.
+template <bool B>
+struct Tag {
+  static constexpr bool value = B;
+  static constexpr bool is_dynamic = false;
+};
+struct Dyn {
+  bool value;
+  static constexpr bool is_dynamic = true;
+};
+
+// Two 8-byte transposed LDS reads -> one 16-byte MFMA operand.
+__device__ __forceinline__ u32x4 lds_read_tr16x2(const unsigned char* base, int off0, int off1) {
+  i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + off0));
+  i16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + off1));
+  u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
+template <typename E, int D, int BM, int BN, int GH, bool LSE>
+__global__ __launch_bounds__(64 * (BM / 32) * GH)
+__attribute__((amdgpu_waves_per_eu(fwd_waves_per_simd<D, BM, BN, GH>(), fwd_waves_per_simd<D, BM, BN, GH>())))
+void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse,
+                int B, int H, int Hkv, int S, float scale_log2) {
+  constexpr int WR = BM / 32;
+  constexpr int NW = WR * GH;
+  constexpr int NB = BN / 32;          // 32-key blocks per tile
+  constexpr int KT = D / 16;           // MFMA k-steps over D
+  constexpr int DB = D / 32;           // 32-row blocks of O^T
+  constexpr int ROWB = D * 2;          // bytes per K/V row
+  constexpr int TILE = BN * ROWB;      // bytes per K or V tile
+  constexpr int NBLK = TILE / 1024;    // 1 KB DMA blocks per tile
+  constexpr int CPR = ROWB / 16;       // 16-byte chunks per row
+  constexpr int NDMA = (NBLK + NW - 1) / NW;  // DMA blocks per wave per tile (K and V each)
+  static_assert(TILE % 1024 == 0, "tile must be whole 1 KB DMA blocks");
+  const float NEG_INF = -__builtin_inff();
+
+  // K buffers at [0, 2 TILE), V buffers at [2 TILE, 4 TILE)
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[4 * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 31, hh = lane >> 5;
+  const int wh = wave % GH, wr = wave / GH;
+
+  // ---- work item: (batch, head group, query tile), heavy first, XCD aware
+  const int nq = S / BM;
+  const int units_per_b = H / GH;
+  const int total = B * units_per_b * nq;
+  const int wg = blockIdx.x;
+  const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
+  const int unit = L / nq;
+  const int qt = nq - 1 - (L % nq);
+  const int b = unit / units_per_b;
+  const int h0 = (unit % units_per_b) * GH;
+  const int hq = h0 + wh;
+  const int hkv = h0 / (H / Hkv);
+
+  const unsigned char* Kbh = reinterpret_cast<const unsigned char*>(K + (size_t)(b * Hkv + hkv) * S * D);
+  const unsigned char* Vbh = reinterpret_cast<const unsigned char*>(V + (size_t)(b * Hkv + hkv) * S * D);
+  const size_t qbase = (size_t)(b * H + hq) * S * D;
+
+  const int r0 = qt * BM;          // first query row of this workgroup
+  const int q0 = r0 + wr * 32;     // first query row of this wave
+  const int m = q0 + c;            // this lane's query row
+  const int ntiles = (r0 + BM + BN - 1) / BN;
+  const int jfull = r0 / BN;       // tiles wholly below the workgroup's first row
+
+  // ---- DMA of one K/V tile into an LDS buffer: 1 KB per wave instruction,
+  // lane L's 16 bytes land at block + 16 L; the lane loads the global bytes
+  // that belong there under the swizzles above.  A lane's source offsets inside
+  // a tile are fixed (kvo / vvo); the tile offset j*TILE is a scalar (soffset).
+  const int drow = lane / CPR;                 // row inside a 1 KB block
+  const int dpos = (lane % CPR) * 16;          // LDS byte offset inside the row
+  int kvo[NDMA], vvo[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int row = (wave + i * NW) * (1024 / ROWB) + drow;
+    kvo[i] = row * ROWB + (((dpos >> 4) ^ ((row * CPR / 16) & (CPR - 1))) << 4);
+    vvo[i] = row * ROWB + (dpos ^ ((32 * (row & 3)) & (ROWB - 1)));
+  }
+  const auto krs = make_rsrc(Kbh, S * ROWB);
+  const auto vrs = make_rsrc(Vbh, S * ROWB);
+  auto dma_k = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int blk = wave + i * NW;
+      if (NBLK % NW == 0 || blk < NBLK) dma16(krs, buf + blk * 1024, kvo[i], j * TILE);
+    }
+  };
+  auto dma_v = [&](int j, unsigned char* buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int blk = wave + i * NW;
+      if (NBLK % NW == 0 || blk < NBLK) dma16(vrs, buf + blk * 1024, vvo[i], j * TILE);
+    }
+  };
+
+  // ---- Q^T operand in registers: k-step t holds Q[m][16t + 8hh .. +7]
+  u32x4 qf[KT];
+  {
+    const uint16_t* qrow = Q + qbase + (size_t)m * D + 8 * hh;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) qf[t] = gload16(qrow + 16 * t);
+  }
+
+  // ---- per-lane LDS operand offsets
+  // K A-operand, k-step t: row c (+ 32 nb), chunk (2t+hh) ^ kswz(c)
+  int koff[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) koff[t] = c * ROWB + (((2 * t + hh) ^ ((c * CPR / 16) & (CPR - 1))) << 4);
+  // V^T A-operand via transposed reads: in 16-lane group G, lane (kr, c4) addresses
+  // key row 4hh + kr (+ block offsets) and the 4 columns feeding output lanes
+  // 4c4..4c4+3, which hold d = pi(16(G&1) + 4c4) + 0..3 of the 32-d block.
+  int voff_even, voff_odd;
+  {
+    const int G = lane >> 4, kr = (lane >> 2) & 3, c4 = lane & 3;
+    const int e = 2 * pi_swap23(16 * (G & 1) + 4 * c4);     // byte offset < 64
+    const int k1 = (ROWB >= 128) ? (kr >> 1) : 0;
+    const int base = (4 * hh + kr) * ROWB + (e ^ (32 * (kr & 1)));
+    voff_even = base + 64 * k1;           // (64 db + e) ^ 32 kr for even db, minus 64 db
+    voff_odd = base + 64 * (1 - k1) - 64;  // same for odd db
+  }
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+  float mrun = NEG_INF, lrun = 0.f;
+
+  // ---- pipeline stages.  `mt` is Tag<false> for tiles wholly below the
+  // diagonal (everything compile-time) or Dyn for the generic path, where
+  // `mt.value` says whether the tile straddles the diagonal (wave-uniform).
+  // Valid 32-key blocks of a tile for this wave (<= 0: none).
+  auto valid_blocks = [&](int k0, auto mt) __attribute__((always_inline)) {
+    if (!mt.value) return NB;
+    const int n = (q0 + 32 - k0) / 32;
+    return n > NB ? NB : n;
+  };
+
+  // S^T = K Q^T: A row c <- key 32nb + c; register g of lane (c, hh) holds
+  // key offset 8*(g/4) + 4*hh + (g%4) of the block, query c.  Keys past the
+  // query are set to -inf on the diagonal block.
+  auto s_tile = [&](const unsigned char* Ks, int k0, int nv, auto mt, f32x16 (&s)[NB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (!mt.value || nb < nv) {
+        f32x16 x = f32x16{};
+#pragma unroll
+        for (int t = 0; t < KT; ++t) x = mfma32<E>(lds_read16(Ks, koff[t] + nb * 32 * ROWB), qf[t], x);
+        if (mt.value && k0 + 32 * nb == q0) {
+#pragma unroll
+          for (int g = 0; g < 16; ++g) {
+            const int koffs = 8 * (g >> 2) + 4 * hh + (g & 3);
+            if (koffs > c) x[g] = NEG_INF;
+          }
+        }
+        s[nb] = x;
+      }
+    }
+  };
+
+  // Row max of a tile in scaled log2 units (-inf where the wave has no valid block).
+  auto tile_max = [&](const f32x16 (&s)[NB], int nv, auto mt) __attribute__((always_inline)) {
+    float mx = NEG_INF;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      if (!mt.value || nb < nv) {
+#pragma unroll
+        for (int g = 0; g < 16; ++g) mx = fmaxf(mx, s[nb][g]);
+      }
+    return halfwave_max(mx) * scale_log2;
+  };
+
+  // Move the reference point to mx (or keep it if larger): rescale acc and l.
+  auto rescale_to = [&](float mx) __attribute__((always_inline)) {
+    const float mnew = fmaxf(mrun, mx);
+    const float alpha = fast_exp2(mrun - mnew);
+    mrun = mnew;
+    lrun *= alpha;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 16; ++g) acc[db][g] *= alpha;
+  };
+
+  // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
+  // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7);
+  // returns this lane's sum of the rounded P (v_dot2c with (1, 1)).
+  auto exp_tile = [&](const f32x16 (&s)[NB], int nv, auto mt, u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
+    float lsum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if (!mt.value || nb < nv) {
+        float p[16];
+#pragma unroll
+        for (int g = 0; g < 16; ++g) p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          u32x4 w;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+            lsum[i1] = add_pair<E>(w[q], lsum[i1]);
+          }
+          pk[2 * nb + i1] = w;
+        }
+      }
+    }
+    return lsum[0] + lsum[1];
+  };
+
+  // P of a tile against the lazy reference point, and the l update.  The
+  // first tile always takes the slow path (m = -inf gives p = inf).
+  auto softmax = [&](const f32x16 (&s)[NB], int nv, auto mt, u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
+    float ts = exp_tile(s, nv, mt, pk);
+    if (__builtin_amdgcn_ballot_w64(!(ts <= kSumLimit))) {
+      rescale_to(tile_max(s, nv, mt));
+      ts = exp_tile(s, nv, mt, pk);
+    }
+    lrun += ts;
+  };
+
+  // O^T += V^T P^T; operand rows are d = 32db + pi(row), keys per slot as above.
+  auto pv = [&](const unsigned char* Vs, const u32x4 (&pk)[2 * NB], int nv, auto mt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int vb = ((db & 1) ? voff_odd : voff_even) + 64 * db;
+#pragma unroll
+      for (int u = 0; u < 2 * NB; ++u) {
+        if (!mt.value || (u >> 1) < nv) {
+          const int o = vb + 16 * u * ROWB;
+          acc[db] = mfma32<E>(lds_read_tr16x2(Vs, o, o + 8 * ROWB), pk[u], acc[db]);
+        }
+      }
+    }
+  };
+
+  // ---- software pipeline over key tiles.  Iteration j: wait for K(j+1) and
+  // V(j), start the DMA of K(j+2) and V(j+1), then S(j+1) on the MFMA pipe
+  // while the VALU turns S(j) into P(j), then PV(j).  K runs one tile ahead of
+  // V; both are double-buffered.
+  auto Kbuf = [&](int j) __attribute__((always_inline)) { return lds + (j & 1) * TILE; };
+  auto Vbuf = [&](int j) __attribute__((always_inline)) { return lds + 2 * TILE + (j & 1) * TILE; };
+
+  auto iteration = [&](int j, f32x16 (&sc)[NB], int nvc, f32x16 (&sn)[NB], int& nvn, auto mt) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (j + 2 < ntiles) dma_k(j + 2, Kbuf(j));
+    if (j + 1 < ntiles) dma_v(j + 1, Vbuf(j + 1));
+    const Dyn cur{j >= jfull};
+    u32x4 pk[2 * NB];
+    if (!mt.value || j + 1 < ntiles) {
+      const Dyn nxt{j + 1 >= jfull};
+      nvn = mt.value ? valid_blocks((j + 1) * BN, nxt) : NB;
+      if constexpr (decltype(mt)::is_dynamic) {
+        s_tile(Kbuf(j + 1), (j + 1) * BN, nvn, nxt, sn);
+        softmax(sc, nvc, cur, pk);
+        pv(Vbuf(j), pk, nvc, cur);
+      } else {
+        s_tile(Kbuf(j + 1), (j + 1) * BN, NB, mt, sn);
+        softmax(sc, NB, mt, pk);
+        pv(Vbuf(j), pk, NB, mt);
+      }
+    } else {
+      softmax(sc, nvc, cur, pk);
+      pv(Vbuf(j), pk, nvc, cur);
+    }
+  };
+
+  // prologue: K(0), V(0), K(1) in flight; S(0)
+  dma_k(0, Kbuf(0));
+  dma_v(0, Vbuf(0));
+  if (ntiles > 1) dma_k(1, Kbuf(1));
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  f32x16 sa[NB], sb[NB];
+  int nva, nvb = NB;
+  {
+    const Dyn m0{jfull == 0};
+    nva = valid_blocks(0, m0);
+    s_tile(Kbuf(0), 0, nva, m0, sa);
+  }
+
+  // tiles j with j + 1 < jfull: both S(j) and S(j+1) below the diagonal
+  int j = 0;
+  for (; j + 2 < jfull; j += 2) {
+    iteration(j, sa, NB, sb, nvb, Tag<false>{});
+    iteration(j + 1, sb, NB, sa, nva, Tag<false>{});
+  }
+  for (; j < ntiles; j += 2) {
+    iteration(j, sa, nva, sb, nvb, Dyn{true});
+    if (j + 1 < ntiles) iteration(j + 1, sb, nvb, sa, nva, Dyn{true});
+  }
+
+  // ---- epilogue: O = acc / l; lane holds d = 32db + 16i1 + 8hh + 0..7
+  const float ltot = halfwave_sum(lrun);
+  const float inv = 1.0f / ltot;
+  uint16_t* orow = O + qbase + (size_t)m * D;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1) {
+      gstore16(orow + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, inv));
+    }
+  }
+  if (LSE && hh == 0) Lse[(size_t)(b * H + hq) * S + m] = mrun + __log2f(ltot);
+}
+
+// ---------------------------------------------------------------------------
+template <typename E, int D, int BM, int BN, int GH, bool LSE>
+static int launch_fwd(const FwdArgs& a) {
+  constexpr int NT = 64 * (BM / 32) * GH;
+  const int total = a.B * (a.H / GH) * (a.S / BM);
+  hipLaunchKernelGGL((fwd_kernel<E, D, BM, BN, GH, LSE>), dim3(total), dim3(NT), 0, (hipStream_t)a.stream,
+                     (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v,
+                     (uint16_t*)a.o, a.lse, a.B, a.H, a.Hkv, a.S, a.scale_log2);
+  return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+}
+
+// Dispatch over the compile-time parameters of one (element type, D) slice.
+template <typename E, int D>
+static FwdFn pick_fwd(int bm, int bn, int gh, bool lse) {
+#define FA_CASE(BM_, BN_, GH_)                                                          \
+  if (bm == BM_ && bn == BN_ && gh == GH_)                                             \
+    return lse ? launch_fwd<E, D, BM_, BN_, GH_, true> : launch_fwd<E, D, BM_, BN_, GH_, false>;
+  FA_CASE(64, 64, 1) FA_CASE(64, 128, 1) FA_CASE(128, 64, 1) FA_CASE(128, 128, 1)
+  FA_CASE(64, 64, 2) FA_CASE(64, 128, 2) FA_CASE(128, 64, 2)
+  FA_CASE(64, 64, 4)
+#undef FA_CASE
+  return nullptr;
+}
+
+}  // namespace fa
+
+// FA_ETYPE (fa::F16 / fa::BF16), FA_D and FA_FWD_TABLE come from the build.
+extern "C" FA_HIDDEN fa::FwdFn FA_FWD_TABLE(int bm, int bn, int gh, int lse) {
+  return fa::pick_fwd<FA_ETYPE, FA_D>(bm, bn, gh, lse != 0);
+}

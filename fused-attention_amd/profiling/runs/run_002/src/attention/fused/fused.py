@@ -1,0 +1,29 @@
+"""Fused causal MHA forward on MI355X: drop-in for attention/fused/fused.py:68-76.
+
+    O = fused_attention(q, k, v, tile_m=64, tile_n=64)
+
+q, k, v: [B, H, N, D] float16 or bfloat16 GPU tensors.  Returns O with q's
+shape and dtype, enqueued on the current stream without synchronising (as the
+reference's ct.launch).  tile_m / tile_n select the kernel's query rows per
+workgroup and keys per LDS tile (each 64 or 128).  N may be any length: a
+partial last tile is masked (the reference raises ValueError unless N is a
+multiple of both tiles, attention/fused/fused.py:70-71).
+"""
+
+import torch
+
+from attention import _lib
+
+
+def fused_attention(q, k, v, tile_m=64, tile_n=64):
+    B, H, N, D = q.shape
+    _lib.check_tiles(tile_m, tile_n)
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must all be (B, H, N, D); got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v must share one dtype; got {q.dtype}, {k.dtype}, {v.dtype}")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    o = torch.empty_like(q)
+    _lib.fwd(q, k, v, o, None, tile_m, tile_n)
+    return o

@@ -1,0 +1,240 @@
+// fa_api.hip - the extern "C" entry points declared in include/fa.h.
+//
+// Argument checking mirrors the reference's host wrappers
+// (attention/fused/fused.py:69-71, attention/gqa/fused_gqa.py:71-77,
+// attention/backward/fused_backward.py:151-158); the Python layer raises the
+// reference's exception types before it ever reaches this ABI, so these
+// checks are the last line of defence for C callers.
+#include <atomic>
+#include <cstdint>
+
+#include "fa_launch.h"
+
+namespace {
+
+constexpr int kMaxGroupHeadsPerWg = 4;
+
+bool tile_ok(int t) { return t == 64 || t == 128; }
+
+fa::FwdFn fwd_table(int dtype, int D, int bm, int bn, int gh, int lse) {
+  if (dtype == FA_F16) {
+    if (D == 32) return fa_fwd_table_f16_32(bm, bn, gh, lse);
+    if (D == 64) return fa_fwd_table_f16_64(bm, bn, gh, lse);
+    if (D == 128) return fa_fwd_table_f16_128(bm, bn, gh, lse);
+  } else if (dtype == FA_BF16) {
+    if (D == 32) return fa_fwd_table_bf16_32(bm, bn, gh, lse);
+    if (D == 64) return fa_fwd_table_bf16_64(bm, bn, gh, lse);
+    if (D == 128) return fa_fwd_table_bf16_128(bm, bn, gh, lse);
+  }
+  return nullptr;
+}
+
+fa::BwdFn bwd_table(int dtype, int D, int bm, int bn) {
+  if (dtype == FA_F16) {
+    if (D == 32) return fa_bwd_table_f16_32(bm, bn);
+    if (D == 64) return fa_bwd_table_f16_64(bm, bn);
+    if (D == 128) return fa_bwd_table_f16_128(bm, bn);
+  } else if (dtype == FA_BF16) {
+    if (D == 32) return fa_bwd_table_bf16_32(bm, bn);
+    if (D == 64) return fa_bwd_table_bf16_64(bm, bn);
+    if (D == 128) return fa_bwd_table_bf16_128(bm, bn);
+  }
+  return nullptr;
+}
+
+// Query heads per workgroup for a GQA group: as many heads of one K/V group
+// as fit in 8 waves (512 threads), each head taking block_m/32 waves.  With
+// 128-key tiles a wave holds two 128-key score tiles in flight and needs more
+// than the 256 VGPRs of two waves per SIMD, so the workgroup stays at 4 waves.
+int heads_per_wg(int group, int block_m, int block_n) {
+  int cap = (block_n == 128 ? 128 : 256) / block_m;  // waves / (block_m / 32)
+  if (cap > kMaxGroupHeadsPerWg) cap = kMaxGroupHeadsPerWg;
+  int gh = 1;
+  while (gh * 2 <= cap && group % (gh * 2) == 0) gh *= 2;
+  return gh;
+}
+
+int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n) {
+  if (B <= 0 || H <= 0 || S <= 0) return FA_ERR_DIMS;
+  if (dtype != FA_F16 && dtype != FA_BF16) return FA_ERR_DTYPE;
+  if (D != 32 && D != 64 && D != 128) return FA_ERR_HEADDIM;
+  if (!tile_ok(block_m) || !tile_ok(block_n)) return FA_ERR_TILE;  // any S >= 1: partial edge tiles
+  // element offsets inside one tensor are formed in 32-bit for the per-row
+  // parts and 64-bit for the (batch, head) base; keep the whole tensor
+  // addressable with 32-bit row indices
+  if ((long long)B * H * S > 0x7fffffffLL) return FA_ERR_DIMS;
+  return FA_OK;
+}
+
+// CU count of the current device, read once per device: the launch paths ask on
+// every call, and a short call is bound by host time.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  int cus = (dev >= 0 && dev < kMaxDevices) ? g_cus[dev].load(std::memory_order_relaxed) : 0;
+  if (cus <= 0) {
+    if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    else if (dev < kMaxDevices)
+      g_cus[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
+// Forward query heads per workgroup for this launch: heads_per_wg's choice, but
+// four heads (64-row tiles) drop to two when the grid would hold fewer than four
+// workgroups per CU, where the heavy-first order cannot balance the causal
+// triangle (B=2 H=8 H_kv=1 S=8192 fp16, tile 64x64: D=128 0.328 -> 0.288 ms,
+// D=32 0.175 -> 0.123 ms; at B=2 H=32 H_kv=8, 2048 workgroups, four stay 3 %
+// faster).  Two heads of 64 rows still hold two waves per SIMD.
+int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
+  int gh = heads_per_wg(group, block_m, block_n);
+  if (gh == 4 && (long long)B * (H / 4) * ((S + block_m - 1) / block_m) < 4LL * cu_count()) gh = 2;
+  return gh;
+}
+
+// tile_m only sets how many 32-row waves share a workgroup: each 32-row group runs
+// the same arithmetic over the same key tiles either way, so results do not depend
+// on it (bitwise).  A single-head workgroup of 64 rows holds two waves, and with
+// its K and V tiles double-buffered in LDS it gets one wave per SIMD
+// or less; where that is measured slower, tile_m = 64 runs as 128-row workgroups.
+// Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows: tile_n = 64:
+// D=128 685 -> 970, D=64 582 -> 809, D=32 358 -> 552; tile_n = 128: D=128 350 -> 637
+// (D <= 64 about equal, so left).  dQ: D = 128 only (both tile_n).
+int fwd_block_m(int block_m, int block_n, int D, int gh) {
+  return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
+}
+int dq_block_m(int block_m, int D) { return (block_m == 64 && D == 128) ? 128 : block_m; }
+
+// Workgroups the dK/dV kernel should have for its heavy-first order to balance:
+// two rounds of one workgroup per CU (a split costs an fp32 partial write, read
+// and reduction, so it is kept to what load balance needs).
+int dkdv_target_workgroups() { return 2 * cu_count(); }
+
+size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
+  return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
+}
+
+// -LSE/c and -Delta per query row ([2, B*H, S] fp32), rounded up to 256 bytes so
+// the partial sums after them stay aligned
+size_t rowb_bytes(int B, int H, int S) {
+  return (2 * (size_t)B * H * S * sizeof(float) + 255) / 256 * 256;
+}
+
+// Chunks per key tile for dK/dV: enough that B * H_kv * (key tiles) * nsplit
+// reaches the target number of workgroups, at most the pairs of the heaviest key
+// tile (G query heads x all 64-row query tiles) and kMaxDkdvSplit; 1 when the key
+// tiles alone already fill the GPU, or when the heaviest tile has fewer than
+// kMinSplitPairs pairs: then the partial-sum traffic and the extra pass cost more
+// than the imbalance (measured: B=2 H=8 S=2048 D=128 0.133 ms whole, 0.146 ms split;
+// B=1 H=8 S=4096 0.241 -> 0.217 ms; MQA H=32 S=4096 3.17 -> 0.42 ms).
+constexpr int kMaxDkdvSplit = 64;
+constexpr int kMinSplitPairs = 64;
+int dkdv_nsplit(int B, int H, int H_kv, int S) {
+  const long long items = (long long)B * H_kv * ((S + fa::kDkdvKeys - 1) / fa::kDkdvKeys);
+  const long long want = dkdv_target_workgroups();
+  const long long pairs = (long long)(H / H_kv) * ((S + 63) / 64);
+  if (items >= want || pairs < kMinSplitPairs) return 1;
+  long long s = (want + items - 1) / items;
+  if (s > pairs) s = pairs;
+  if (s > kMaxDkdvSplit) s = kMaxDkdvSplit;
+  return s < 1 ? 1 : (int)s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+           int B, int H, int H_kv, int S, int D, int dtype, float scale_log2,
+           int block_m, int block_n, void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, block_m, block_n);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
+  if (!q || !k || !v || !o) return FA_ERR_NULL;
+  const int gh = fwd_heads_per_wg(B, H, H / H_kv, S, block_m, block_n);
+  fa::FwdFn fn = fwd_table(dtype, D, fwd_block_m(block_m, block_n, D, gh), block_n, gh, lse != nullptr);
+  if (!fn) return FA_ERR_UNSUPPORTED;
+  fa::FwdArgs a{q, k, v, o, lse, B, H, H_kv, S, D, scale_log2, hip_stream};
+  return fn(a);
+}
+
+int fa_bwd(const void* q, const void* k, const void* v, const void* o,
+           const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+           int B, int H, int S, int D, int dtype, float scale_log2, float sm_scale,
+           int block_m, int block_n, void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, block_m, block_n);
+  if (st != FA_OK) return st;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  fa::BwdFn fn = bwd_table(dtype, D, dq_block_m(block_m, D), block_n);
+  if (!fn) return FA_ERR_UNSUPPORTED;
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream,
+                nullptr, nullptr, 1, nullptr};
+  return fn(a);
+}
+
+size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D) {
+  if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
+  if (D != 32 && D != 64 && D != 128) return 0;
+  return rowb_bytes(B, H, S) + gqa_workspace_bytes(B, H_kv, S, D, dkdv_nsplit(B, H, H_kv, S));
+}
+
+int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
+               const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+               int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+               int block_m, int block_n, void* workspace, size_t workspace_bytes, void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, block_m, block_n);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15)) return FA_ERR_WORKSPACE;
+  fa::BwdFn fn = bwd_table(dtype, D, dq_block_m(block_m, D), block_n);
+  if (!fn) return FA_ERR_UNSUPPORTED;
+  // the workspace holds, in this order and as far as it reaches: the per-row terms
+  // (dQ then runs first and dK/dV reads Delta instead of forming it), then the
+  // partial sums of the split the shape asks for, or of the largest one that fits
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  size_t left = workspace ? workspace_bytes : 0;
+  float* rowb = nullptr;
+  if (left >= rowb_bytes(B, H, S)) {
+    rowb = reinterpret_cast<float*>(ws);
+    ws += rowb_bytes(B, H, S);
+    left -= rowb_bytes(B, H, S);
+  }
+  int nsplit = workspace ? dkdv_nsplit(B, H, H_kv, S) : 1;
+  while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > left) --nsplit;
+  float* wsk = nsplit > 1 ? reinterpret_cast<float*>(ws) : nullptr;
+  float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
+                wsk, wsv, nsplit, rowb};
+  return fn(a);
+}
+
+int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with_lse, int is_bwd) {
+  if (check_common(1, 1, 256, D, dtype, block_m, block_n) != FA_OK) return 0;
+  if (group <= 0) return 0;
+  if (is_bwd) return bwd_table(dtype, D, block_m, block_n) ? 1 : 0;
+  return fwd_table(dtype, D, block_m, block_n, heads_per_wg(group, block_m, block_n), with_lse) ? 1 : 0;
+}
+
+const char* fa_strerror(int status) {
+  switch (status) {
+    case FA_OK: return "ok";
+    case FA_ERR_DIMS: return "invalid dimensions (B, H, H_kv, S must be positive and H_kv must divide H)";
+    case FA_ERR_DTYPE: return "unsupported dtype (expected float16 or bfloat16)";
+    case FA_ERR_HEADDIM: return "unsupported head dim (expected 32, 64 or 128)";
+    case FA_ERR_TILE: return "unsupported tile (block_m and block_n must be 64 or 128)";
+    case FA_ERR_NULL: return "a required pointer is NULL";
+    case FA_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FA_ERR_UNSUPPORTED: return "no kernel for this combination";
+    case FA_ERR_WORKSPACE: return "workspace not 16-byte aligned";
+    default: return "unknown status";
+  }
+}
+
+int fa_version(void) { return 140; }
+
+}  // extern "C"

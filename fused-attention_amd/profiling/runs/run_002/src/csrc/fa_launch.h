@@ -1,0 +1,84 @@
+// fa_launch.h - host-side launch plumbing shared by the kernel translation units
+// and the C ABI (fa_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include "../../include/fa.h"
+
+namespace fa {
+
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int B, H, Hkv, S, D;
+  float scale_log2;
+  void* stream;
+};
+
+struct BwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* d_o;
+  const float* lse;
+  void* dq;
+  void* dk;
+  void* dv;
+  int B, H, Hkv, S, D;
+  float scale_log2;
+  float sm_scale;
+  void* stream;
+  // the (query tile, query head) pairs of a key tile are split over `nsplit`
+  // workgroups, each writing fp32 partial dK / dV ([B*Hkv*nsplit, S, D] each) that a
+  // reduction pass adds up; nsplit = 1: one workgroup, no workspace
+  float* wsk;
+  float* wsv;
+  int nsplit;
+  // [2, B*H, S] fp32: -LSE/c and -Delta of every query row, written by the dQ
+  // kernel (then launched first) for the dK/dV kernel; null: dK/dV forms them
+  float* rowb;
+};
+
+// keys per dK/dV workgroup (4 waves x 32 keys), for the split heuristics on the host
+constexpr int kDkdvKeys = 128;
+
+typedef int (*FwdFn)(const FwdArgs&);
+typedef int (*BwdFn)(const BwdArgs&);
+
+// Raise the dynamic LDS limit of a kernel once (needed above 64 KB).  The
+// static local makes the first call per kernel instance thread-safe.
+template <int SMEM>
+inline bool smem_attr(const void* kern) {
+  if (SMEM <= 65536) return true;
+  return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, SMEM) == hipSuccess;
+}
+
+#define set_smem_once(kern, SMEM)                                   \
+  ([&]() {                                                          \
+    static const bool ok_ = ::fa::smem_attr<SMEM>(kern);            \
+    return ok_;                                                     \
+  }())
+
+}  // namespace fa
+
+#define FA_HIDDEN __attribute__((visibility("hidden")))
+
+// Per-slice dispatch tables, one translation unit per (element type, D).
+extern "C" {
+FA_HIDDEN fa::FwdFn fa_fwd_table_f16_32(int bm, int bn, int gh, int lse);
+FA_HIDDEN fa::FwdFn fa_fwd_table_f16_64(int bm, int bn, int gh, int lse);
+FA_HIDDEN fa::FwdFn fa_fwd_table_f16_128(int bm, int bn, int gh, int lse);
+FA_HIDDEN fa::FwdFn fa_fwd_table_bf16_32(int bm, int bn, int gh, int lse);
+FA_HIDDEN fa::FwdFn fa_fwd_table_bf16_64(int bm, int bn, int gh, int lse);
+FA_HIDDEN fa::FwdFn fa_fwd_table_bf16_128(int bm, int bn, int gh, int lse);
+FA_HIDDEN fa::BwdFn fa_bwd_table_f16_32(int bm, int bn);
+FA_HIDDEN fa::BwdFn fa_bwd_table_f16_64(int bm, int bn);
+FA_HIDDEN fa::BwdFn fa_bwd_table_f16_128(int bm, int bn);
+FA_HIDDEN fa::BwdFn fa_bwd_table_bf16_32(int bm, int bn);
+FA_HIDDEN fa::BwdFn fa_bwd_table_bf16_64(int bm, int bn);
+FA_HIDDEN fa::BwdFn fa_bwd_table_bf16_128(int bm, int bn);
+}

@@ -37,6 +37,7 @@ import json
 import os
 import platform
 import re
+import shlex
 import socket
 import statistics
 import subprocess
@@ -46,6 +47,10 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(HERE)
 DEFAULT_KERNEL = "attention/fused/fused.py"
+# what a forward run measures besides the kernel file: the library sources behind
+# fused_attention, snapshotted into run_NNN/src/ so the next run can diff against them
+# even where git is absent (the GPU machine)
+DEFAULT_SOURCES = "csrc/fa_fwd.hip,csrc/fa_api.hip,csrc/fa_device.h,csrc/fa_launch.h"
 CSV_FIELDS = ["run", "timestamp", "gpu", "commit", "kernel", "note", "D", "N", "B", "H",
               "impl", "tile_m", "tile_n", "median_ms", "tflops", "dtype", "pct_peak"]
 PEAK_TFLOPS = 2516.6  # MI355X dense bf16/fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
@@ -129,7 +134,9 @@ class Records:
         with open(os.path.join(run_dir, "env.json"), "w") as f:
             json.dump({"run": run, "timestamp": ts, "note": note, "env": env}, f, indent=2)
         for name, text in (extra_files or {}).items():
-            with open(os.path.join(run_dir, name), "w") as f:
+            path = os.path.join(run_dir, name)
+            os.makedirs(os.path.dirname(path), exist_ok=True)
+            with open(path, "w") as f:
                 f.write(text)
 
 
@@ -403,26 +410,48 @@ def run_profile(args, run_dir):
 
 
 # --------------------------------------------------------------------------- code diff
-def kernel_source_at(commit, kernel):
-    src = sh(f"git show {commit}:{kernel}") if commit and commit != "unknown" else ""
-    if not src and os.path.exists(kernel):
-        src = open(kernel).read()
-    return src
+def snap_name(path):
+    """Where a measured source is kept inside run_NNN/src/: its path below the package root
+    (a file outside the package keeps only its name)."""
+    rel = os.path.relpath(os.path.join(PKG_ROOT, path), PKG_ROOT)
+    return os.path.basename(path) if rel.startswith("..") else rel
 
 
-def code_diff(history, gpu, run, kernel_path):
+def source_at(commit, path):
+    """path (relative to the package root) at a git commit, or '' where that is unknown."""
+    if not commit or commit == "unknown":
+        return ""
+    return sh(f"git -C {shlex.quote(PKG_ROOT)} show {shlex.quote(commit)}:./{shlex.quote(path)}")
+
+
+def previous_sources(records_dir, out_dir, prev, row, paths):
+    """{path: text} of the previous run: its src/ snapshot, else git at its commit."""
+    snap = os.path.join(out_dir or os.path.join(records_dir, "runs"), f"run_{prev:03d}", "src")
+    commit = ((row or {}).get("commit") or "").split(" ")[0]
+    out = {}
+    for pth in paths:
+        f = os.path.join(snap, snap_name(pth))
+        out[pth] = open(f).read() if os.path.exists(f) else source_at(commit, pth)
+    return out
+
+
+def code_diff(history, gpu, run, paths, records_dir, out_dir=None):
+    """(previous run, unified diff of every measured source) or None when the previous
+    run's sources are not known (no snapshot and no usable commit)."""
     prev = find_ref(history, gpu, run, "prev")
     if prev is None:
         return None
     row = next((r for r in history if int(r["run"]) == prev), None)
-    prev_kernel = (row or {}).get("kernel") or DEFAULT_KERNEL
-    prev_src = kernel_source_at(((row or {}).get("commit") or "").split(" ")[0], prev_kernel)
-    if not prev_src:
+    old = previous_sources(records_dir, out_dir, prev, row, paths)
+    if not any(old.values()):
         return None
-    cur = open(kernel_path).read()
-    d = "".join(difflib.unified_diff(prev_src.splitlines(True), cur.splitlines(True),
-                                     fromfile=f"Run {prev}: {prev_kernel}", tofile=f"Run {run}: {kernel_path}", n=2))
-    return prev, (d.rstrip("\n") or "(no code changes)")
+    parts = []
+    for pth in paths:
+        cur = open(os.path.join(PKG_ROOT, pth)).read() if os.path.exists(os.path.join(PKG_ROOT, pth)) else ""
+        parts.append("".join(difflib.unified_diff(old[pth].splitlines(True), cur.splitlines(True),
+                                                  fromfile=f"Run {prev}: {pth}", tofile=f"Run {run}: {pth}", n=2)))
+    d = "".join(parts).rstrip("\n")
+    return prev, (d or "(no code changes)")
 
 
 # --------------------------------------------------------------------------- report
@@ -517,6 +546,9 @@ def parse_args(argv=None):
     p.add_argument("--change", default="", help="what was changed, in words (the code diff is added)")
     p.add_argument("--kernel", default=DEFAULT_KERNEL, help="Python file defining fused_attention(q, k, v, tile_m, tile_n)")
     p.add_argument("--records-dir", default=HERE, help="where runs.csv, RUNS.md and runs/ live")
+    p.add_argument("--sources", default=DEFAULT_SOURCES,
+                   help="comma-separated library sources (relative to the package root) snapshotted with "
+                        "the kernel file and diffed against the previous run")
     p.add_argument("--out-dir", default="", help="folder for run_NNN/ (default: <records-dir>/runs)")
     p.add_argument("--no-check", action="store_true", help="skip the correctness gate")
     p.add_argument("--B", type=int, default=2)
@@ -538,7 +570,7 @@ def parse_args(argv=None):
     p.add_argument("--import-csv", help="record an existing benchmark CSV as a run instead of measuring")
     p.add_argument("--timestamp", help="for --import-csv: 'YYYY-MM-DD HH:MM' (UTC)")
     p.add_argument("--gpu", help="for --import-csv: GPU name")
-    p.add_argument("--commit", help="for --import-csv: git commit of the measured code")
+    p.add_argument("--commit", help="git commit of the measured code (for --import-csv, or where git is absent)")
     p.add_argument("--_profile-target", dest="profile_target", action="store_true", help=argparse.SUPPRESS)
     return p.parse_args(argv)
 
@@ -568,6 +600,8 @@ def main(argv=None):
     ts = now_utc()
     env = collect_env(args)
     env["kernel"] = args.kernel
+    if args.commit:
+        env["commit"] = args.commit
     if not args.no_check:
         print(f"Checking {args.kernel} against the fp32 reference ...")
         if not check_correctness(load_fused(args.kernel), parse_tiles(args.tiles), torch_dtype(args.dtype), args.B, args.H):
@@ -577,9 +611,11 @@ def main(argv=None):
     rows = measure(args, impls, parse_tiles(args.tiles))
     run_dir = rec.run_dir(run, args.out_dir)
     profile, logs = (run_profile(args, run_dir) if args.profile else (None, []))
-    diff = code_diff(history, env["gpu"], run, args.kernel)
+    paths = [args.kernel] + [x for x in args.sources.split(",") if x]
+    diff = code_diff(history, env["gpu"], run, paths, args.records_dir, args.out_dir)
     md = build_markdown(run, ts, env, args.note, rows, history, profile, args.reason, args.change, diff)
-    extra = {}
+    extra = {os.path.join("src", snap_name(pth)): open(os.path.join(PKG_ROOT, pth)).read()
+             for pth in paths if os.path.exists(os.path.join(PKG_ROOT, pth))}
     if diff:
         extra["change.diff"] = diff[1] + "\n"
     if logs:

@@ -96,3 +96,23 @@ def test_cli_parsing_keeps_reference_flags():
     assert a.profile and a.profile_size == "128,4096" and a.profile_tile == "128x64"
     assert tr.parse_tiles(a.tiles) == [(64, 64), (128, 64)] and tr.parse_list("64,128") == [64, 128]
     assert tr.change(0.8, 1.0) == "20.0% faster" and tr.change(1.25, 1.0) == "25.0% slower" and tr.change(1, None) == "-"
+
+
+def test_code_diff_uses_the_previous_runs_source_snapshot(tmp_path, monkeypatch):
+    """Where git is absent (the GPU machine) the diff comes from run_NNN/src/ of the previous
+    run; without a snapshot or a usable commit no diff is claimed."""
+    pkg = tmp_path / "pkg"
+    (pkg / "csrc").mkdir(parents=True)
+    (pkg / "csrc" / "k.hip").write_text("a\nb\nc\n")
+    monkeypatch.setattr(tr, "PKG_ROOT", str(pkg))
+    rec_dir = tmp_path / "records"
+    history = [{"run": "1", "gpu": "G", "commit": "unknown"}]
+    assert tr.code_diff(history, "G", 2, ["csrc/k.hip"], str(rec_dir)) is None
+    snap = rec_dir / "runs" / "run_001" / "src" / "csrc"
+    snap.mkdir(parents=True)
+    (snap / "k.hip").write_text("a\nb\nc\n")
+    assert tr.code_diff(history, "G", 2, ["csrc/k.hip"], str(rec_dir)) == (1, "(no code changes)")
+    (pkg / "csrc" / "k.hip").write_text("a\nB\nc\n")
+    prev, d = tr.code_diff(history, "G", 2, ["csrc/k.hip"], str(rec_dir))
+    assert prev == 1 and "-b" in d and "+B" in d and "Run 1: csrc/k.hip" in d
+    assert tr.snap_name("/elsewhere/x.py") == "x.py"
