@@ -99,8 +99,8 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
 // tile_m only sets how many 32-row waves share a workgroup: each 32-row group runs
 // the same arithmetic over the same key tiles either way, so results do not depend
 // on it (bitwise).  A single-head workgroup of 64 rows holds two waves, and with
-// its K and V tiles double-buffered in LDS it gets one wave per SIMD
-// or less; where that is measured slower, tile_m = 64 runs as 128-row workgroups.
+// its K and V tiles double-buffered in LDS it gets one wave per SIMD or less;
+// where that is measured slower, tile_m = 64 runs as 128-row workgroups.
 // Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows: tile_n = 64:
 // D=128 685 -> 970, D=64 582 -> 809, D=32 358 -> 552; tile_n = 128: D=128 350 -> 637
 // (D <= 64 about equal, so left).  dQ: D = 128 only (both tile_n).
