@@ -15,7 +15,8 @@ Prints one JSON line.  `roofline` is the forward kernel's achieved TFLOP/s
 (algorithmic FLOPs / mean kernel duration from HIP events around each launch
 on the launch stream) against the dense bf16 MFMA peak; `cpu_baseline` is the
 reference's fp32 PyTorch path (oracle/cpu_reference.py) timed on the host cores
-on a bounded slice of the same workload.
+on a bounded slice of the same workload, and `fwd_bwd.cpu_baseline` fp32 autograd of
+the same formula (forward + backward) on a bounded slice.
 """
 
 import argparse
@@ -102,44 +103,63 @@ def time_steps(fn, steps, warmup, torch, warm_seconds):
     return wall_ms / steps, statistics.mean(per), statistics.median(per)
 
 
-def cpu_baseline(args, torch):
-    """The reference's fp32 PyTorch formula on the host cores, over a bounded head slice."""
-    from oracle.cpu_reference import reference_attention_explicit
-
-    S, D = WORKLOAD["S"], WORKLOAD["D"]
-    g = torch.Generator().manual_seed(0)
-    heads = 1
-    q = torch.randn(1, heads, S, D, generator=g).bfloat16().float()
-    k = torch.randn(1, heads, S, D, generator=g).bfloat16().float()
-    v = torch.randn(1, heads, S, D, generator=g).bfloat16().float()
-    t0 = time.perf_counter()
-    reference_attention_explicit(q, k, v)  # warm-up
-    one = time.perf_counter() - t0
-    # grow the head count so the median-of-3 run takes about --cpu-seconds in total
-    heads = int(max(1, min(WORKLOAD["B"] * WORKLOAD["H"], args.cpu_seconds / 3 / max(one, 1e-3))))
-    q = torch.randn(1, heads, S, D, generator=g).bfloat16().float()
-    k = torch.randn(1, heads, S, D, generator=g).bfloat16().float()
-    v = torch.randn(1, heads, S, D, generator=g).bfloat16().float()
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        reference_attention_explicit(q, k, v)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    tflops = causal_fwd_flops(1, heads, S, D) / t / 1e12
-    cpu = "unknown"
+def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"reference fp32 explicit formula, B=1 H={heads} S={S} D={D} of the bf16 workload "
-                      f"(values rounded to bf16), median of 3 after 1 warm-up; {t:.2f} s per pass; "
-                      f"host {cpu}, os.cpu_count()={os.cpu_count()}"}
+    return "unknown"
+
+
+def _time_cpu(fn, make_inputs, seconds, max_heads, torch):
+    """Median of 3 timed passes of fn over a head slice sized so the three take about
+    `seconds` (one warm-up pass on one head sets the size).  Returns (heads, seconds per pass)."""
+    fn(*make_inputs(1))  # warm-up
+    t0 = time.perf_counter()
+    fn(*make_inputs(1))
+    one = time.perf_counter() - t0
+    heads = int(max(1, min(max_heads, seconds / 3 / max(one, 1e-3))))
+    inputs = make_inputs(heads)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn(*inputs)
+        times.append(time.perf_counter() - t0)
+    return heads, statistics.median(times)
+
+
+def cpu_baseline(args, torch):
+    """The reference's fp32 PyTorch formula on the host cores, over a bounded head slice:
+    forward (oracle.cpu_reference.reference_attention_explicit, the path of
+    attention/fused/reference.py:16-23) and forward+backward by fp32 autograd of the same
+    formula (oracle.cpu_reference.reference_grads, as tests/backward/run_correctness_backward.py:25-44)."""
+    from oracle.cpu_reference import reference_attention_explicit, reference_grads
+
+    S, D = WORKLOAD["S"], WORKLOAD["D"]
+    g = torch.Generator().manual_seed(0)
+
+    def make(heads, n=3):
+        return [torch.randn(1, heads, S, D, generator=g).bfloat16().float() for _ in range(n)]
+
+    host = f"host {_cpu_model()}, os.cpu_count()={os.cpu_count()}"
+    heads, t = _time_cpu(reference_attention_explicit, make, args.cpu_seconds, WORKLOAD["B"] * WORKLOAD["H"], torch)
+    fwd = {"value": round(causal_fwd_flops(1, heads, S, D) / t / 1e12, 4), "unit": "TFLOP/s",
+           "cores": torch.get_num_threads(), "kind": "port",
+           "sample": f"reference fp32 explicit formula, B=1 H={heads} S={S} D={D} of the bf16 workload "
+                     f"(values rounded to bf16), median of 3 after 1 warm-up; {t:.2f} s per pass; {host}"}
+    if args.no_bwd:
+        return fwd, None
+    # autograd holds a few N x N fp32 tensors per head: at most 16 heads (about 6 GB) per pass
+    heads, t = _time_cpu(lambda q, k, v, do: reference_grads(q, k, v, do), lambda h: make(h, 4),
+                         args.cpu_seconds, 16, torch)
+    fb = {"value": round(3.5 * causal_fwd_flops(1, heads, S, D) / t / 1e12, 4), "unit": "TFLOP/s",
+          "cores": torch.get_num_threads(), "kind": "port",
+          "sample": f"fp32 autograd of the reference's explicit formula (forward + backward), B=1 H={heads} "
+                    f"S={S} D={D} of the bf16 workload, 3.5x causal FLOP convention, median of 3 after "
+                    f"1 warm-up; {t:.2f} s per pass; {host}"}
+    return fwd, fb
 
 
 def main():
@@ -202,6 +222,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic_from_profile(),
+                     "traffic_source": "profiles/" + os.path.basename(TRAFFIC_FILE) + " (rocprofv3 --pmc "
+                                       "FETCH_SIZE and WRITE_SIZE runs of bench.py --traffic-run; not "
+                                       "measured in this run)",
                      "kernel": "fa::fwd_kernel", "kernel_ms_mean": round(kern_ms_mean, 4),
                      "kernel_ms_median": round(kern_ms_med, 4),
                      "algorithmic_bytes": 4 * B * H * S * D * 2},
@@ -225,7 +248,9 @@ def main():
         result["fwd_bwd"] = None
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args, torch)
+        result["cpu_baseline"], fb_cpu = cpu_baseline(args, torch)
+        if result["fwd_bwd"] is not None:
+            result["fwd_bwd"]["cpu_baseline"] = fb_cpu
     else:
         result["cpu_baseline"] = None
     result["host"] = {"python": platform.python_version(), "torch": torch.__version__,

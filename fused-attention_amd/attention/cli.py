@@ -15,6 +15,7 @@ Differences, all widenings:
 """
 
 import argparse
+import os
 import sys
 import time
 
@@ -42,20 +43,28 @@ def parse_args(argv, description):
 
 
 def load_qkv(path, ValidationError):
-    """Load Q, K, V from an .npz file, raising ValidationError for missing or malformed files."""
-    try:
-        with np.load(path, allow_pickle=False) as data:
-            missing = [key for key in ("Q", "K", "V") if key not in data.files]
-            if missing:
-                raise ValidationError(
-                    f"{path} is missing array(s) {', '.join(missing)}; found {sorted(data.files)}")
-            return data["Q"], data["K"], data["V"]
-    except FileNotFoundError:
+    """The Q, K and V arrays of an .npz archive.
+
+    Every way the file can be unusable -- absent, not an archive, or lacking one of the
+    three keys -- becomes the caller's ValidationError, whose text is the CLI's message
+    (exit code 2); pickled members are refused."""
+    if not os.path.exists(path):
         raise ValidationError(f"input file not found: {path}")
+    try:
+        archive = np.load(path, allow_pickle=False)
     except (OSError, ValueError) as e:
-        if isinstance(e, ValidationError):
-            raise
         raise ValidationError(f"could not read {path} as .npz: {e}")
+    with archive:
+        names = getattr(archive, "files", None)
+        if names is None:  # a bare .npy array, not an archive of named arrays
+            raise ValidationError(f"could not read {path} as .npz: not an archive of named arrays")
+        absent = [name for name in ("Q", "K", "V") if name not in names]
+        if absent:
+            raise ValidationError(f"{path} is missing array(s) {', '.join(absent)}; found {sorted(names)}")
+        try:
+            return tuple(archive[name] for name in ("Q", "K", "V"))
+        except (OSError, ValueError) as e:
+            raise ValidationError(f"could not read {path} as .npz: {e}")
 
 
 def input_dtypes(backend, compute_dtype):

@@ -63,6 +63,9 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
   // parts and 64-bit for the (batch, head) base; keep the whole tensor
   // addressable with 32-bit row indices
   if ((long long)B * H * S > 0x7fffffffLL) return FA_ERR_DIMS;
+  // the kernels form byte offsets inside one (batch, head) slice, and the byte
+  // size of a slice's remaining rows, in 32-bit int: keep S * D * 2 below 2^31
+  if ((long long)S * D * 2 > 0x7fffffffLL) return FA_ERR_DIMS;
   return FA_OK;
 }
 
@@ -223,7 +226,9 @@ int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with
 const char* fa_strerror(int status) {
   switch (status) {
     case FA_OK: return "ok";
-    case FA_ERR_DIMS: return "invalid dimensions (B, H, H_kv, S must be positive and H_kv must divide H)";
+    case FA_ERR_DIMS:
+      return "invalid dimensions (B, H, H_kv, S must be positive, H_kv must divide H, B*H*S and "
+             "S*D*2 must stay below 2^31)";
     case FA_ERR_DTYPE: return "unsupported dtype (expected float16 or bfloat16)";
     case FA_ERR_HEADDIM: return "unsupported head dim (expected 32, 64 or 128)";
     case FA_ERR_TILE: return "unsupported tile (block_m and block_n must be 64 or 128)";

@@ -49,7 +49,8 @@ PKG_ROOT = os.path.dirname(HERE)
 DEFAULT_KERNEL = "attention/fused/fused.py"
 # what a forward run measures besides the kernel file: the library sources behind
 # fused_attention, snapshotted into run_NNN/src/ so the next run can diff against them
-# even where git is absent (the GPU machine)
+# even where git is absent (the GPU machine); the snapshots are working files, kept out
+# of version control (change.diff records what changed)
 DEFAULT_SOURCES = "csrc/fa_fwd.hip,csrc/fa_api.hip,csrc/fa_device.h,csrc/fa_launch.h"
 CSV_FIELDS = ["run", "timestamp", "gpu", "commit", "kernel", "note", "D", "N", "B", "H",
               "impl", "tile_m", "tile_n", "median_ms", "tflops", "dtype", "pct_peak"]
@@ -78,10 +79,12 @@ def now_utc():
 
 
 def git_commit():
-    c = sh("git rev-parse --short HEAD")
-    if c and sh("git status --porcelain --untracked-files=no"):
-        c += " (+ uncommitted changes)"
-    return c or "unknown"
+    """Abbreviated HEAD, marked when tracked files differ from it; 'unknown' without git."""
+    desc = sh(f"git -C {shlex.quote(PKG_ROOT)} describe --always --abbrev=10 --dirty=+dirty")
+    if not desc:
+        return "unknown"
+    head, dirty = desc.split("+")[0], desc.endswith("+dirty")
+    return head + (" (+ uncommitted changes)" if dirty else "")
 
 
 def parse_list(s, cast=int):
@@ -467,27 +470,30 @@ def find_ref(history, gpu, run, which):
 
 
 def change(new_ms, old_ms):
-    if old_ms is None:
+    """Relative time change of a row against an earlier run's same row, in words."""
+    if old_ms is None or old_ms <= 0:
         return "-"
-    pct = (old_ms - new_ms) / old_ms * 100
-    return f"{abs(pct):.1f}% {'faster' if pct >= 0 else 'slower'}"
+    saved = 1.0 - new_ms / old_ms
+    word = "faster" if saved >= 0 else "slower"
+    return f"{100.0 * abs(saved):.1f}% {word}"
 
 
 def build_markdown(run, ts, env, note, rows, history, profile=None, reason="", change_txt="", diff=None):
     gpu = env.get("gpu", "")
     prev, base = find_ref(history, gpu, run, "prev"), find_ref(history, gpu, run, "first")
     hist = {(int(r["run"]),) + key_of(r): float(r["median_ms"]) for r in history}
+    # heading, then the optional narrative sections (the reference's RUNS.md layout)
+    sections = [(None, [f"**Note:** {note}"] if note else []),
+                ("Why (from profiling)", [reason] if reason else []),
+                ("Change", ([change_txt] if change_txt else [])
+                 + ([f"Code diff vs Run {diff[0]}:", "", "```diff", diff[1], "```"] if diff else []))]
     L = [f"## Run {run} — {ts} UTC", ""]
-    if note:
-        L += [f"**Note:** {note}", ""]
-    if reason:
-        L += ["### Why (from profiling)", "", reason, ""]
-    if change_txt or diff:
-        L += ["### Change", ""]
-        if change_txt:
-            L += [change_txt, ""]
-        if diff:
-            L += [f"Code diff vs Run {diff[0]}:", "", "```diff", diff[1], "```", ""]
+    for title, body in sections:
+        if not body:
+            continue
+        if title:
+            L += [f"### {title}", ""]
+        L += body + [""]
     labels = [("kernel", "Kernel file"), ("gpu", "GPU"), ("gfx_arch", "Architecture"),
               ("compute_units", "Compute units"), ("gpu_memory_gb", "GPU memory (GB)"),
               ("rocm_smi_clocks", "rocm-smi clocks"), ("torch", "PyTorch"), ("torch_hip", "HIP"),

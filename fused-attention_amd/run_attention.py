@@ -27,18 +27,35 @@ from attention.fused.validation import ValidationError, validate_qkv  # noqa: E4
 BACKENDS = cli.BACKENDS
 
 
+def _hip_backend():
+    from attention.fused.fused import fused_attention
+    return fused_attention
+
+
+def _unfused_backend():
+    from attention.fused.unfused import unfused_attention
+    return lambda q, k, v, bm, bn: unfused_attention(q, k, v, bm, bn)
+
+
+def _reference_backend():
+    from attention.fused.reference import causal_attention_reference
+    return lambda q, k, v, bm, bn: causal_attention_reference(q, k, v)
+
+
+# backend name -> factory; modules are imported only when their backend is picked, so the
+# reference backend runs where no GPU library can load ("cutile" names the fused HIP path,
+# as the reference's command lines expect)
+_FACTORIES = {"hip": _hip_backend, "cutile": _hip_backend, "unfused": _unfused_backend,
+              "reference": _reference_backend}
+
+
 def get_backend(name):
-    """Return fn(q, k, v, block_m, block_n) -> torch.Tensor [B, H, N, D]. Imports lazily."""
-    if name in ("hip", "cutile"):
-        from attention.fused.fused import fused_attention
-        return fused_attention
-    if name == "unfused":
-        from attention.fused.unfused import unfused_attention
-        return lambda q, k, v, bm, bn: unfused_attention(q, k, v, bm, bn)
-    if name == "reference":
-        from attention.fused.reference import causal_attention_reference
-        return lambda q, k, v, bm, bn: causal_attention_reference(q, k, v)
-    raise NotImplementedError(f"backend '{name}' is not implemented")
+    """The attention callable of backend `name`, called as fn(q, k, v, block_m, block_n) and
+    returning O with q's [B, H, N, D] shape (run_attention.py:62-73 in the reference)."""
+    factory = _FACTORIES.get(name)
+    if factory is None:
+        raise NotImplementedError(f"backend '{name}' is not implemented")
+    return factory()
 
 
 def main(argv=None) -> int:

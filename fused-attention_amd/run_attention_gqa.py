@@ -25,18 +25,34 @@ from attention.gqa.validation_gqa import ValidationError, validate_qkv  # noqa: 
 BACKENDS = cli.BACKENDS
 
 
+def _hip_backend():
+    from attention.gqa.fused_gqa import fused_gqa_attention
+    return fused_gqa_attention
+
+
+def _unfused_backend():
+    from attention.gqa.unfused_gqa import unfused_gqa_attention
+    return lambda q, k, v, bm, bn: unfused_gqa_attention(q, k, v, bm, bn)
+
+
+def _reference_backend():
+    from attention.gqa.reference_gqa import causal_attention_reference_gqa
+    return lambda q, k, v, bm, bn: causal_attention_reference_gqa(q, k, v)
+
+
+# backend name -> factory (imports deferred to the pick; "cutile" names the fused HIP path)
+_FACTORIES = {"hip": _hip_backend, "cutile": _hip_backend, "unfused": _unfused_backend,
+              "reference": _reference_backend}
+
+
 def get_backend(name):
-    """Return fn(q, k, v, block_m, block_n) -> torch.Tensor [B, H, N, D]. Imports lazily."""
-    if name in ("hip", "cutile"):
-        from attention.gqa.fused_gqa import fused_gqa_attention
-        return fused_gqa_attention
-    if name == "unfused":
-        from attention.gqa.unfused_gqa import unfused_gqa_attention
-        return lambda q, k, v, bm, bn: unfused_gqa_attention(q, k, v, bm, bn)
-    if name == "reference":
-        from attention.gqa.reference_gqa import causal_attention_reference_gqa
-        return lambda q, k, v, bm, bn: causal_attention_reference_gqa(q, k, v)
-    raise NotImplementedError(f"backend '{name}' is not implemented")
+    """The grouped-query attention callable of backend `name`, called as
+    fn(q, k, v, block_m, block_n) with K/V of H_kv heads, returning O shaped like q
+    (run_attention_gqa.py:64-75 in the reference)."""
+    factory = _FACTORIES.get(name)
+    if factory is None:
+        raise NotImplementedError(f"backend '{name}' is not implemented")
+    return factory()
 
 
 def main(argv=None) -> int:

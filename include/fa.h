@@ -29,7 +29,8 @@ enum fa_dtype { FA_F16 = 0, FA_BF16 = 1 };
 
 enum fa_status {
   FA_OK = 0,
-  FA_ERR_DIMS = -1,     /* B, H, H_kv or S not positive, or H % H_kv != 0 */
+  FA_ERR_DIMS = -1,     /* B, H, H_kv or S not positive, H % H_kv != 0, or
+                           B*H*S or S*D*2 (bytes of one head's rows) >= 2^31 */
   FA_ERR_DTYPE = -2,    /* dtype is neither FA_F16 nor FA_BF16 */
   FA_ERR_HEADDIM = -3,  /* D not in {32, 64, 128} */
   FA_ERR_TILE = -4,     /* block_m / block_n not in {64, 128} */

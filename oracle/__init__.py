@@ -27,5 +27,12 @@ something other than a retyped formula):
                     reference's lists (84 / 96 / 7); planted-mistake tests show
                     the checks fail for a wrong sign, a dropped scale or a
                     transposed operand
+cpu_reference (tests/test_cpu_reference.py) is pinned against the float64 oracle above:
+  explicit formula  MHA, GQA and MQA shapes, plus row 0 == V[0] and the prefix means of Q = 0
+  head chunking     budgets that split the heads into ragged chunks and whole GQA groups
+                    (g = 1, 2, 4, 8), equal to one unchunked pass; mutated copies (wrong
+                    K/V head index, chunks straddling a group, the last K/V head rounded
+                    down, a shifted output slice) are caught
+  fp32 autograd     dQ, dK, dV for MHA and GQA (group sums), the single 1/sqrt(D) factor
 No function is left "parity unpinned".
 """

@@ -75,6 +75,15 @@ def test_fwd_rejects_bad_arguments(lib, kw, code):
     assert fwd(lib, **kw) == code
 
 
+@pytest.mark.parametrize("S,D", [(1 << 23, 128), (1 << 24, 64), (1 << 25, 32), ((1 << 23) + 5, 128)])
+def test_rows_of_one_head_past_2gib_are_rejected(lib, S, D):
+    """S * D * 2 bytes of one (batch, head) slice must stay below 2^31: the kernels form
+    byte offsets and tile sizes inside a slice in 32-bit int.  B = H = 1 keeps B*H*S legal."""
+    assert fwd(lib, B=1, H=1, Hkv=1, S=S, D=D) == _lib.FA_ERR_DIMS
+    assert bwd(lib, B=1, H=1, S=S, D=D) == _lib.FA_ERR_DIMS
+    assert bwd_gqa(lib, B=1, H=1, Hkv=1, S=S, D=D) == _lib.FA_ERR_DIMS
+
+
 @pytest.mark.parametrize("kw,code", [
     (dict(H=0), _lib.FA_ERR_DIMS),
     (dict(dtype=7), _lib.FA_ERR_DTYPE),
