@@ -116,6 +116,7 @@ class Records:
         return os.path.join(out_dir or os.path.join(self.root, "runs"), f"run_{run:03d}")
 
     def append(self, run, ts, env, note, rows, markdown, run_dir, extra_files=None):
+        os.makedirs(self.root, exist_ok=True)
         os.makedirs(run_dir, exist_ok=True)
         new = not os.path.exists(self.csv)
         with open(self.csv, "a", newline="") as f:
@@ -178,7 +179,7 @@ def load_fused(kernel_path):
         from attention.fused.fused import fused_attention
         return fused_attention
     import importlib.util
-    path = os.path.abspath(kernel_path)
+    path = os.path.abspath(kernel_path if os.path.exists(kernel_path) else os.path.join(PKG_ROOT, kernel_path))
     name = "tracked_" + re.sub(r"\W", "_", os.path.splitext(os.path.basename(path))[0])
     spec = importlib.util.spec_from_file_location(name, path)
     mod = importlib.util.module_from_spec(spec)
@@ -601,7 +602,8 @@ def main(argv=None):
         rec.append(run, ts, env, args.note, rows, md, rec.run_dir(run, args.out_dir))
         print(md)
         return 0
-    if not os.path.exists(args.kernel):
+    # a relative kernel path names a file below the working directory or the package root
+    if not os.path.exists(args.kernel) and not os.path.exists(os.path.join(PKG_ROOT, args.kernel)):
         sys.exit(f"kernel file not found: {args.kernel}")
     ts = now_utc()
     env = collect_env(args)

@@ -116,3 +116,12 @@ def test_code_diff_uses_the_previous_runs_source_snapshot(tmp_path, monkeypatch)
     prev, d = tr.code_diff(history, "G", 2, ["csrc/k.hip"], str(rec_dir))
     assert prev == 1 and "-b" in d and "+B" in d and "Run 1: csrc/k.hip" in d
     assert tr.snap_name("/elsewhere/x.py") == "x.py"
+
+
+def test_records_create_their_folder(tmp_path):
+    """A records folder that does not exist yet (runs kept elsewhere) is created on the first run."""
+    rec = tr.Records(str(tmp_path / "new" / "records"))
+    env = {"gpu": "g", "commit": "c", "kernel": tr.DEFAULT_KERNEL}
+    md = tr.build_markdown(1, "t", env, "n", rows_for(1.0), [])
+    rec.append(1, "t", env, "n", rows_for(1.0), md, str(tmp_path / "elsewhere" / "run_001"))
+    assert len(rec.history()) == 1 and os.path.exists(rec.md)
