@@ -28,6 +28,7 @@ FA_ERR_NULL = -5
 FA_ERR_LAUNCH = -6
 FA_ERR_UNSUPPORTED = -7
 FA_ERR_WORKSPACE = -8
+FA_ERR_SCRATCH = -9
 
 # (name, restype, argtypes) for every symbol of include/fa.h
 _VP, _I, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
@@ -37,6 +38,9 @@ SIGNATURES = {
                     _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
     "fa_bwd_gqa": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                         _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP, ctypes.c_size_t, _VP]),
+    "fa_bwd_gqa_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                                _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
+    "fa_noalloc_scratch_bytes": (ctypes.c_size_t, []),
     "fa_bwd_gqa_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "fa_supported": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "fa_strerror": (ctypes.c_char_p, [_I]),
@@ -107,7 +111,8 @@ def check(code, what):
     msg = f"{what}: {strerror(code)} (status {code})"
     if code == FA_ERR_DTYPE:
         raise TypeError(msg)
-    if code in (FA_ERR_DIMS, FA_ERR_HEADDIM, FA_ERR_TILE, FA_ERR_NULL, FA_ERR_UNSUPPORTED, FA_ERR_WORKSPACE):
+    if code in (FA_ERR_DIMS, FA_ERR_HEADDIM, FA_ERR_TILE, FA_ERR_NULL, FA_ERR_UNSUPPORTED, FA_ERR_WORKSPACE,
+                FA_ERR_SCRATCH):
         raise ValueError(msg)
     raise RuntimeError(msg)
 

@@ -7,6 +7,7 @@
 // checks are the last line of defence for C callers.
 #include <atomic>
 #include <cstdint>
+#include <mutex>
 
 #include "fa_launch.h"
 
@@ -147,6 +148,40 @@ int dkdv_nsplit(int B, int H, int H_kv, int S) {
   return s < 1 ? 1 : (int)s;
 }
 
+// ---------------------------------------------------------------------------
+// Device scratch of the allocation-free backward (fa_bwd_gqa_noalloc): stands in
+// for fa_bwd_gqa's caller workspace.  Each device that loads the library holds its
+// own copy until the process ends.  On the host the array's name is only a
+// stand-in for the symbol, never a device address: host code uses the address
+// that hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// This device's copy of `scratch`, looked up on the first call on the device (with
+// it current) and kept; FA_ERR_LAUNCH if the runtime cannot name it.
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FA_ERR_LAUNCH;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return FA_ERR_LAUNCH;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -216,6 +251,28 @@ int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
   return fn(a);
 }
 
+int fa_bwd_gqa_noalloc(const void* q, const void* k, const void* v, const void* o,
+                       const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+                       int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+                       int block_m, int block_n, void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, block_m, block_n);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  // the workspace fa_bwd_gqa would take for this shape must fit the scratch whole: the
+  // same per-row terms and the same split, hence the same kernels and the same results.
+  // Nothing in it needs clearing: dQ writes every row's terms before dK/dV reads them,
+  // and every split chunk stores its whole partial sum before the reduction reads it.
+  if (fa_bwd_gqa_workspace_size(B, H, H_kv, S, D) > kNoAllocScratchBytes) return FA_ERR_SCRATCH;
+  void* ws = nullptr;
+  st = scratch_address(&ws);
+  if (st != FA_OK) return st;
+  return fa_bwd_gqa(q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, dtype, scale_log2, sm_scale,
+                    block_m, block_n, ws, kNoAllocScratchBytes, hip_stream);
+}
+
+size_t fa_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
 int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with_lse, int is_bwd) {
   if (check_common(1, 1, 256, D, dtype, block_m, block_n) != FA_OK) return 0;
   if (group <= 0) return 0;
@@ -236,6 +293,9 @@ const char* fa_strerror(int status) {
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_UNSUPPORTED: return "no kernel for this combination";
     case FA_ERR_WORKSPACE: return "workspace not 16-byte aligned";
+    case FA_ERR_SCRATCH:
+      return "this shape needs more workspace than the library's device scratch (fa_bwd_gqa_noalloc); "
+             "use fa_bwd_gqa with a caller workspace";
     default: return "unknown status";
   }
 }

@@ -37,7 +37,8 @@ enum fa_status {
   FA_ERR_NULL = -5,     /* a required pointer is NULL */
   FA_ERR_LAUNCH = -6,   /* the HIP runtime rejected a launch */
   FA_ERR_UNSUPPORTED = -7, /* valid arguments, but no kernel for this combination */
-  FA_ERR_WORKSPACE = -8    /* fa_bwd_gqa: workspace not 16-byte aligned */
+  FA_ERR_WORKSPACE = -8,   /* fa_bwd_gqa: workspace not 16-byte aligned */
+  FA_ERR_SCRATCH = -9      /* fa_bwd_gqa_noalloc: shape needs more than the library's scratch */
 };
 
 /*
@@ -117,6 +118,31 @@ FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o
                const void* d_o, const float* lse, void* dq, void* dk, void* dv,
                int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
                int block_m, int block_n, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/*
+ * fa_bwd_gqa for callers that cannot allocate device memory -- code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc.  No counterpart in the
+ * reference.  Same arguments and results as fa_bwd_gqa(..., workspace, bytes, stream)
+ * given a workspace of fa_bwd_gqa_workspace_size() bytes (bitwise: the same kernels
+ * with the same split), but the workspace is the library's own device scratch, a
+ * static array of fa_noalloc_scratch_bytes() = 64 MiB that each device holds from the
+ * library's first use on it until the process ends.  The call allocates nothing (no
+ * hipMalloc, no hipFree, no allocating library routine).
+ *   Limit: shapes whose fa_bwd_gqa_workspace_size() exceeds 64 MiB are rejected with
+ *   FA_ERR_SCRATCH before anything is enqueued (8 * B * H * S bytes of per-row terms,
+ *   plus the split's partial sums: e.g. B * H * S <= 8M with no split).
+ *   Every call on a device shares that device's scratch: calls whose work overlaps on
+ *   one device (different streams, or host threads without ordering) race; serialise
+ *   them on one stream.  Nothing in the scratch needs to start at zero.
+ */
+FA_API int fa_bwd_gqa_noalloc(const void* q, const void* k, const void* v, const void* o,
+                       const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+                       int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+                       int block_m, int block_n, void* hip_stream);
+
+/* Bytes of the device scratch behind fa_bwd_gqa_noalloc (per device).  No reference
+ * counterpart. */
+FA_API size_t fa_noalloc_scratch_bytes(void);
 
 /* Workspace bytes fa_bwd_gqa uses for this shape on the current device: the
  * per-row terms, plus the partial sums when the key tiles alone leave the GPU

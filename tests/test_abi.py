@@ -39,7 +39,7 @@ def test_no_internal_symbols_leak():
 
 
 def test_strerror_covers_every_status(lib):
-    for code in range(0, -9, -1):
+    for code in range(0, -10, -1):
         assert lib.fa_strerror(code).decode() not in ("", "unknown status")
     assert lib.fa_strerror(-99).decode() == "unknown status"
 
@@ -168,3 +168,27 @@ def test_no_unresolved_library_symbols():
     out = os.popen(f"nm -D --undefined-only {_lib.LIB_PATH}").read()
     missing = [line.split()[-1] for line in out.splitlines() if "_ZN2fa" in line]
     assert not missing, missing[:5]
+
+
+def test_noalloc_entry_rejects_shapes_past_its_scratch(lib):
+    """fa_bwd_gqa_noalloc: argument errors as fa_bwd_gqa, and FA_ERR_SCRATCH -- before any
+    launch -- when the shape's workspace exceeds the library's 64 MiB device scratch."""
+    assert lib.fa_noalloc_scratch_bytes() == 64 << 20
+
+    def noalloc(B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE):
+        return lib.fa_bwd_gqa_noalloc(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, B, H, Hkv, S, D, dtype,
+                                      0.1, 0.1, bm, bn, NULL)
+    assert noalloc(Hkv=3) == _lib.FA_ERR_DIMS
+    assert noalloc(dtype=4) == _lib.FA_ERR_DTYPE
+    assert noalloc(D=40) == _lib.FA_ERR_HEADDIM
+    assert noalloc(bn=32) == _lib.FA_ERR_TILE
+    assert noalloc(ptr=NULL) == _lib.FA_ERR_NULL
+    assert noalloc(S=1 << 25, D=32, H=1, Hkv=1) == _lib.FA_ERR_DIMS
+    # 8 * B * H * S bytes of per-row terms alone: 4 * 32 * 65537 rows > 8M
+    assert lib.fa_bwd_gqa_workspace_size(4, 32, 32, 65537, 64) > lib.fa_noalloc_scratch_bytes()
+    assert noalloc(B=4, H=32, Hkv=32, S=65537) == _lib.FA_ERR_SCRATCH
+    # a split that would not fit: MQA with few key tiles asks for large fp32 partial sums
+    big = lib.fa_bwd_gqa_workspace_size(1, 32, 1, 16384, 128)
+    assert big > lib.fa_noalloc_scratch_bytes()
+    assert noalloc(B=1, H=32, Hkv=1, S=16384, D=128) == _lib.FA_ERR_SCRATCH
+    assert "scratch" in lib.fa_strerror(_lib.FA_ERR_SCRATCH).decode()
