@@ -41,6 +41,13 @@ SIGNATURES = {
     "fa_bwd_gqa_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                                 _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _VP]),
     "fa_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "fa_fwd_exact": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _VP]),
+    "fa_bwd_gqa_exact": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                              _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _I, _VP, ctypes.c_size_t, _VP]),
+    "fa_fwd_heads_per_wg": (_I, [_I, _I, _I, _I, _I, _I]),
+    "fa_fwd_rows_per_wg": (_I, [_I, _I, _I, _I]),
+    "fa_bwd_dq_rows_per_wg": (_I, [_I, _I]),
+    "fa_bwd_dkdv_split": (_I, [_I, _I, _I, _I]),
     "fa_bwd_gqa_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "fa_supported": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "fa_strerror": (ctypes.c_char_p, [_I]),

@@ -1,0 +1,84 @@
+"""Registers, LDS, scratch and waves per SIMD of every kernel instance, from the compiler.
+
+    python -m benchmarks.kernel_resources [--hipcc /opt/rocm/bin/hipcc] [--out FILE.md]
+
+Compiles each (kernel family, element type, head dim) slice of csrc/ the way the
+Makefile does, adding `-Rpass-analysis=kernel-resource-usage`, and tabulates the
+compiler's own report per kernel: VGPRs, AGPRs, SGPRs, spills, scratch bytes per lane,
+LDS bytes per workgroup and the occupancy in waves per SIMD those allow.  These are the
+static half of the tile study (benchmarks/tile_study.py measures the run-time half with
+rocprofv3 counters).  Needs no GPU.
+"""
+
+import argparse
+import os
+import re
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "csrc")
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "-fvisibility=hidden", "-Wno-unused-command-line-argument",
+         "-Rpass-analysis=kernel-resource-usage", "-c", "-o", os.devnull]
+SLICES = [(e, d) for e in ("bf16", "f16") for d in (128, 64, 32)]
+FIELDS = ["VGPRs", "AGPRs", "TotalSGPRs", "ScratchSize [bytes/lane]", "Occupancy [waves/SIMD]",
+          "SGPRs Spill", "VGPRs Spill", "LDS Size [bytes/block]"]
+
+
+def compile_slice(hipcc, family, etype, D):
+    et = "fa::BF16" if etype == "bf16" else "fa::F16"
+    table = f"-DFA_FWD_TABLE=fa_fwd_table_{etype}_{D}" if family == "fwd" else f"-DFA_BWD_TABLE=fa_bwd_table_{etype}_{D}"
+    src = os.path.join(CSRC, f"fa_{family}.hip")
+    r = subprocess.run([hipcc, *FLAGS, f"-DFA_ETYPE={et}", f"-DFA_D={D}", table, src],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{src} ({etype}, D={D}) failed:\n{r.stderr[-2000:]}")
+    return parse(r.stderr)
+
+
+def demangle(name):
+    try:
+        out = subprocess.run(["c++filt", name], capture_output=True, text=True).stdout.strip()
+    except OSError:
+        return name
+    m = re.match(r"void (fa::\w+<[^>]*>)", out)
+    return m.group(1) if m else out
+
+
+def parse(text):
+    """{mangled kernel name: {field: value}} from the remarks."""
+    kernels, cur = {}, None
+    for line in text.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = kernels.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([^:]+(?:\[[^\]]*\])?): (\S+) \[-Rpass-analysis", line)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = m.group(2)
+    return kernels
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--hipcc", default="/opt/rocm/bin/hipcc")
+    p.add_argument("--out", default="")
+    args = p.parse_args(argv)
+    jobs = [(f, e, d) for f in ("fwd", "bwd") for e, d in SLICES]
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
+        results = list(ex.map(lambda j: compile_slice(args.hipcc, *j), jobs))
+    L = ["| kernel | " + " | ".join(FIELDS) + " |", "|---|" + "---|" * len(FIELDS)]
+    for kernels in results:
+        for name in sorted(kernels, key=demangle):
+            k = kernels[name]
+            L.append(f"| `{demangle(name)}` | " + " | ".join(k.get(f, "-") for f in FIELDS) + " |")
+    text = "\n".join(L) + "\n"
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text)
+    sys.stdout.write(text)
+
+
+if __name__ == "__main__":
+    main()

@@ -273,6 +273,66 @@ int fa_bwd_gqa_noalloc(const void* q, const void* k, const void* v, const void* 
 
 size_t fa_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
+int fa_fwd_exact(const void* q, const void* k, const void* v, void* o, float* lse,
+                 int B, int H, int H_kv, int S, int D, int dtype, float scale_log2,
+                 int block_m, int block_n, int heads_per_wg, void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, block_m, block_n);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
+  // the heads of one workgroup share one K/V head
+  if (heads_per_wg <= 0 || (H / H_kv) % heads_per_wg != 0) return FA_ERR_DIMS;
+  if (!q || !k || !v || !o) return FA_ERR_NULL;
+  fa::FwdFn fn = fwd_table(dtype, D, block_m, block_n, heads_per_wg, lse != nullptr);
+  if (!fn) return FA_ERR_UNSUPPORTED;
+  fa::FwdArgs a{q, k, v, o, lse, B, H, H_kv, S, D, scale_log2, hip_stream};
+  return fn(a);
+}
+
+int fa_bwd_gqa_exact(const void* q, const void* k, const void* v, const void* o,
+                     const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+                     int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+                     int dq_block_m, int dq_block_n, int nsplit, void* workspace, size_t workspace_bytes,
+                     void* hip_stream) {
+  int st = check_common(B, H, S, D, dtype, dq_block_m, dq_block_n);
+  if (st != FA_OK) return st;
+  if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
+  if (nsplit < 1 || nsplit > kMaxDkdvSplit) return FA_ERR_DIMS;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15)) return FA_ERR_WORKSPACE;
+  // the split's partial sums must fit behind the per-row terms; without a workspace
+  // the reference's order runs (dK/dV forming Delta, then dQ)
+  const size_t need = rowb_bytes(B, H, S) + gqa_workspace_bytes(B, H_kv, S, D, nsplit);
+  if (nsplit > 1 && (!workspace || workspace_bytes < need)) return FA_ERR_WORKSPACE;
+  fa::BwdFn fn = bwd_table(dtype, D, dq_block_m, dq_block_n);
+  if (!fn) return FA_ERR_UNSUPPORTED;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const bool rows = workspace && workspace_bytes >= rowb_bytes(B, H, S);
+  float* rowb = rows ? reinterpret_cast<float*>(ws) : nullptr;
+  float* wsk = nsplit > 1 ? reinterpret_cast<float*>(ws + rowb_bytes(B, H, S)) : nullptr;
+  float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
+  fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
+                wsk, wsv, nsplit, rowb};
+  return fn(a);
+}
+
+int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int block_m, int block_n) {
+  if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
+  if (!tile_ok(block_m) || !tile_ok(block_n)) return 0;
+  return fwd_heads_per_wg(B, H, H / H_kv, S, block_m, block_n);
+}
+
+int fa_fwd_rows_per_wg(int block_m, int block_n, int D, int heads_per_wg) {
+  if (!tile_ok(block_m) || !tile_ok(block_n)) return 0;
+  return fwd_block_m(block_m, block_n, D, heads_per_wg);
+}
+
+int fa_bwd_dq_rows_per_wg(int block_m, int D) { return tile_ok(block_m) ? dq_block_m(block_m, D) : 0; }
+
+int fa_bwd_dkdv_split(int B, int H, int H_kv, int S) {
+  if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
+  return dkdv_nsplit(B, H, H_kv, S);
+}
+
 int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with_lse, int is_bwd) {
   if (check_common(1, 1, 256, D, dtype, block_m, block_n) != FA_OK) return 0;
   if (group <= 0) return 0;

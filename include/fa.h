@@ -144,6 +144,35 @@ FA_API int fa_bwd_gqa_noalloc(const void* q, const void* k, const void* v, const
  * counterpart. */
 FA_API size_t fa_noalloc_scratch_bytes(void);
 
+/*
+ * Tile and occupancy studies.  The entry points above pick the workgroup shape by
+ * rules (rows per workgroup, heads per workgroup, dK/dV split); these run the shape
+ * that is asked for, literally, so each rule's rejected variants can be measured
+ * beside its choice (the reference measures every tile as requested:
+ * profiling/3_tile_study/README.md:8-19).  No counterpart in the reference's API.
+ *
+ * fa_fwd_exact: fa_fwd with block_m query rows per head and heads_per_wg query heads
+ *   (of one K/V group) per workgroup, block_n keys per tile.  FA_ERR_UNSUPPORTED when no
+ *   kernel has that shape ((block_m, block_n, heads_per_wg) in {64,128}x{64,128}x{1},
+ *   {64,128}x{64}x{2}, (64,128,2), (64,64,4)).
+ * fa_bwd_gqa_exact: fa_bwd_gqa with the dQ kernel at dq_block_m x dq_block_n and the
+ *   dK/dV key tiles split nsplit ways (1..64; > 1 needs a workspace of
+ *   8*B*H*S (rounded up to 256) + 8*B*H_kv*nsplit*S*D bytes, else FA_ERR_WORKSPACE).
+ * The queries return what fa_fwd / fa_bwd_gqa choose for a shape (0: invalid).
+ */
+FA_API int fa_fwd_exact(const void* q, const void* k, const void* v, void* o, float* lse,
+                 int B, int H, int H_kv, int S, int D, int dtype, float scale_log2,
+                 int block_m, int block_n, int heads_per_wg, void* hip_stream);
+FA_API int fa_bwd_gqa_exact(const void* q, const void* k, const void* v, const void* o,
+                     const void* d_o, const float* lse, void* dq, void* dk, void* dv,
+                     int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
+                     int dq_block_m, int dq_block_n, int nsplit, void* workspace, size_t workspace_bytes,
+                     void* hip_stream);
+FA_API int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int block_m, int block_n);
+FA_API int fa_fwd_rows_per_wg(int block_m, int block_n, int D, int heads_per_wg);
+FA_API int fa_bwd_dq_rows_per_wg(int block_m, int D);
+FA_API int fa_bwd_dkdv_split(int B, int H, int H_kv, int S);
+
 /* Workspace bytes fa_bwd_gqa uses for this shape on the current device: the
  * per-row terms, plus the partial sums when the key tiles alone leave the GPU
  * idle (0 for invalid dimensions).  No reference counterpart. */

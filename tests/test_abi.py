@@ -192,3 +192,41 @@ def test_noalloc_entry_rejects_shapes_past_its_scratch(lib):
     assert big > lib.fa_noalloc_scratch_bytes()
     assert noalloc(B=1, H=32, Hkv=1, S=16384, D=128) == _lib.FA_ERR_SCRATCH
     assert "scratch" in lib.fa_strerror(_lib.FA_ERR_SCRATCH).decode()
+
+
+def test_exact_shape_entries_and_rule_queries(lib):
+    """The study entry points reject what their kernels cannot run, before any launch, and the
+    rule queries return the dispatch choices of fa_fwd / fa_bwd_gqa."""
+    def fwd_exact(B=1, H=8, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, gh=1, ptr=FAKE):
+        return lib.fa_fwd_exact(ptr, ptr, ptr, ptr, NULL, B, H, Hkv, S, D, dtype, 0.1, bm, bn, gh, NULL)
+    assert fwd_exact(gh=0) == _lib.FA_ERR_DIMS
+    assert fwd_exact(gh=3) == _lib.FA_ERR_DIMS       # does not divide the group of 4
+    assert fwd_exact(H=8, Hkv=4, gh=4) == _lib.FA_ERR_DIMS  # group of 2
+    assert fwd_exact(bm=128, bn=128, gh=2) == _lib.FA_ERR_UNSUPPORTED
+    assert fwd_exact(bm=128, bn=64, gh=4) == _lib.FA_ERR_UNSUPPORTED
+    assert fwd_exact(bn=96) == _lib.FA_ERR_TILE
+    assert fwd_exact(ptr=NULL) == _lib.FA_ERR_NULL
+
+    def bwd_exact(B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, nsplit=1, ws=NULL, ws_bytes=0, ptr=FAKE):
+        return lib.fa_bwd_gqa_exact(ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, ptr, B, H, Hkv, S, D, dtype, 0.1, 0.1,
+                                    bm, bn, nsplit, ws, ws_bytes, NULL)
+    assert bwd_exact(nsplit=0) == _lib.FA_ERR_DIMS
+    assert bwd_exact(nsplit=65) == _lib.FA_ERR_DIMS
+    assert bwd_exact(nsplit=2) == _lib.FA_ERR_WORKSPACE          # a split needs its partial sums
+    need = rowb(1, 4, 256) + 2 * 1 * 2 * 2 * 256 * 64 * 4
+    assert bwd_exact(nsplit=2, ws=ctypes.c_void_p(0x10000), ws_bytes=need - 16) == _lib.FA_ERR_WORKSPACE
+    assert bwd_exact(bm=96) == _lib.FA_ERR_TILE
+    assert bwd_exact(ptr=NULL) == _lib.FA_ERR_NULL
+
+    # the rules, as documented beside them in fa_api.hip
+    assert lib.fa_fwd_rows_per_wg(64, 64, 128, 1) == 128 and lib.fa_fwd_rows_per_wg(64, 128, 128, 1) == 128
+    assert lib.fa_fwd_rows_per_wg(64, 128, 64, 1) == 64 and lib.fa_fwd_rows_per_wg(64, 64, 32, 2) == 64
+    assert lib.fa_bwd_dq_rows_per_wg(64, 128) == 128 and lib.fa_bwd_dq_rows_per_wg(64, 64) == 64
+    assert lib.fa_fwd_heads_per_wg(4, 32, 32, 4096, 128, 64) == 1
+    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 64, 64) == 4
+    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 64) == 2
+    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 1024, 64, 64) == 2     # 4 -> 2: under 4 workgroups per CU
+    assert lib.fa_fwd_heads_per_wg(1, 32, 1, 16384, 64, 128) == 2
+    assert lib.fa_bwd_dkdv_split(4, 32, 32, 4096) == 1
+    assert lib.fa_bwd_dkdv_split(1, 32, 1, 4096) == 16   # 32 key tiles, target 512 workgroups
+    assert lib.fa_fwd_heads_per_wg(0, 32, 8, 4096, 64, 64) == 0 and lib.fa_bwd_dkdv_split(1, 4, 3, 64) == 0
