@@ -871,11 +871,13 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();
   };
+  // (full tiles only: j < jfull <= ntiles - 1, so tile j + 1 always exists and its DMA
+  // needs no branch)
   auto step_pipelined = [&](int j, auto par_tag, auto prev) __attribute__((always_inline)) {
     constexpr bool P = decltype(par_tag)::value;
     unsigned char* cur = P ? lds1 : lds0;
     unsigned char* nxt = P ? lds0 : lds1;
-    if (j + 1 < ntiles) dma_tile(j + 1, nxt);
+    dma_tile(j + 1, nxt);
     tile_pipelined(cur, prev);
     __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     __syncthreads();

@@ -368,8 +368,17 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   auto body = [&](int j, const unsigned char* __restrict__ kcur, unsigned char* __restrict__ kdst,
                   const unsigned char* __restrict__ vcur, unsigned char* __restrict__ vdst,
                   f32x16 (&sc)[NB], int nvc, f32x16 (&sn)[NB], int& nvn, auto mt) __attribute__((always_inline)) {
-    if (j + 2 < ntiles) dma_k(j + 2, kdst);
-    if (j + 1 < ntiles) dma_v(j + 1, vdst);
+    // Static (full-tile) iterations run only while tile j + 2 is below the workgroup's
+    // first row (j + 2 < jfull <= ntiles - 1, and j + 3 <= jfull for the second
+    // iteration of a pair), so their DMAs need no test: without the branches the
+    // DMA issue joins the tile's schedule (2.3 % faster at B=4 H=32 S=4096 D=128).
+    if constexpr (decltype(mt)::is_dynamic) {
+      if (j + 2 < ntiles) dma_k(j + 2, kdst);
+      if (j + 1 < ntiles) dma_v(j + 1, vdst);
+    } else {
+      dma_k(j + 2, kdst);
+      dma_v(j + 1, vdst);
+    }
     const Dyn cur{j >= jfull};
     u32x4 pk[2 * NB];
     if (!mt.value || j + 1 < ntiles) {

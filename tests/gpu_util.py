@@ -19,6 +19,51 @@ from oracle import cpu_reference
 ATOL = 2e-2
 RTOL = 2e-2
 MAX_ABS = 2e-2
+REL_FLOOR = 1e-3  # relative error divides by max(|ref|, 1e-3) (tests/fused/run_correctness.py:35)
+
+# Per-case records of the reference's correctness suites, in the reference's CSV layout
+# (tests/fused/run_correctness.py:187-197, tests/gqa/run_correctness_gqa.py,
+# tests/backward/run_correctness_backward.py:110-113): {(file path, columns): [rows]},
+# written by conftest.py at the end of the session.
+RECORDS = {}
+
+FUSED_COLS = ["case", "B", "H", "N", "D", "magnitude", "seed", "max_abs_err", "max_rel_err", "tol_ratio",
+              "time_s", "result", "note"]
+GQA_COLS = ["case", "B", "H", "H_kv", "group", "N", "D", "magnitude", "seed", "max_abs_err", "max_rel_err",
+            "tol_ratio", "time_s", "result", "note"]
+BWD_COLS = ["test", "B", "H", "N", "D", "sigma", "relerr_O", "relerr_dQ", "relerr_dK", "relerr_dV", "result",
+            "fused_ms", "sdpa_ms", "fused_speedup_vs_sdpa"]
+
+
+def record(path, columns, row):
+    RECORDS.setdefault((path, tuple(columns)), []).append([row.get(c, "") for c in columns])
+
+
+def write_records(root):
+    import csv
+    import os
+    written = []
+    for (path, columns), rows in RECORDS.items():
+        full = os.path.join(root, path)
+        os.makedirs(os.path.dirname(full), exist_ok=True)
+        with open(full, "w", newline="") as f:
+            w = csv.writer(f)
+            w.writerow(columns)
+            w.writerows(rows)
+        written.append(full)
+    return written
+
+
+def compare_ref(out, ref):
+    """(max_abs, max_rel, tol_ratio, nonfinite) of out vs ref, as the reference's compare()
+    (tests/fused/run_correctness.py:70-80): a case passes iff tol_ratio <= 1."""
+    out = out.float()
+    nonfinite = int((~torch.isfinite(out)).sum())
+    if nonfinite:
+        return float("inf"), float("inf"), float("inf"), nonfinite
+    err = (out - ref).abs()
+    return (float(err.max()), float((err / ref.abs().clamp_min(REL_FLOOR)).max()),
+            float((err / (ATOL + RTOL * ref.abs())).max()), 0)
 
 
 def log(msg):
@@ -43,11 +88,24 @@ def head_samples(B, H):
     return sorted(picks)
 
 
-def check_forward(out, q, k, v, rows_count=40, label=""):
-    """Assert out (GPU) matches the oracle on sampled rows and the fp32 reference everywhere."""
+def check_forward(out, q, k, v, rows_count=40, label="", case=None, tiles=None, seconds=None):
+    """Assert out (GPU) matches the oracle on sampled rows and the fp32 reference everywhere.
+    With `case` (one of the reference's suite cases) the comparison is also recorded."""
     B, H, N, D = q.shape
     g = H // k.shape[1]
     ref = cpu_reference.reference_chunked(q, k, v)
+    if case is not None:
+        a, rel, rat, nonfinite = compare_ref(out, ref)
+        tile = f"{tiles[0]}x{tiles[1]}"
+        row = dict(case=case.id, B=B, H=H, N=N, D=D, magnitude=case.magnitude, seed=case.seed,
+                   max_abs_err=a, max_rel_err=rel, tol_ratio=rat, time_s=seconds,
+                   result="PASS" if (nonfinite == 0 and rat <= 1.0) else "FAIL",
+                   note=f"{nonfinite} NaN/Inf values" if nonfinite else "")
+        if k.shape[1] == H and not hasattr(case, "H_kv"):
+            record(f"fused/hip/{tile}/correctness_fused_hip_{tile}.csv", FUSED_COLS, row)
+        else:
+            record(f"fused_gqa/hip/{tile}/correctness_fused_gqa_hip_{tile}.csv", GQA_COLS,
+                   dict(row, H_kv=k.shape[1], group=g))
     max_abs, ratio = compare_full(out, ref)
     del ref
     rows = orc.sample_rows(N, count=rows_count)

@@ -22,7 +22,7 @@ from attention.backward.fused_backward import FusedAttentionFn, fused_attention_
 from oracle import attention_oracle as orc
 from oracle import cases
 from oracle.cpu_reference import reference_grads
-from tests.gpu_util import dev, log
+from tests.gpu_util import BWD_COLS, dev, log, record
 
 pytestmark = pytest.mark.gpu
 
@@ -40,7 +40,7 @@ def run_fused(q, k, v, do, tiles):
     return o.detach(), q.grad, k.grad, v.grad
 
 
-def check_grads(q, k, v, do, tiles, label, oracle_heads=2, unit_variance=True):
+def check_grads(q, k, v, do, tiles, label, oracle_heads=2, unit_variance=True, case=None):
     got = run_fused(q, k, v, do, tiles)
     for name, g in zip(("O", "dQ", "dK", "dV"), got):
         assert g.dtype == q.dtype and g.shape == q.shape, name
@@ -54,6 +54,13 @@ def check_grads(q, k, v, do, tiles, label, oracle_heads=2, unit_variance=True):
         # N = 1 the exact dQ and dK are zero (a single key: P = 1, dP = Delta)
         rel = float((g.float() - r).norm() / max(float(r.norm()), MAX_ABS * r.numel() ** 0.5))
         worst[name] = (max_abs, rel)
+    if case is not None:  # the reference's relative error, ||x - ref|| / ||ref|| (run_correctness_backward.py:35-37)
+        rels = [float((g.float() - r).norm() / r.norm().clamp_min(1e-12)) for g, r in zip(got, ref)]
+        B_, H_, N_, D_ = q.shape
+        record(f"backward/backward_hip_{tiles[0]}x{tiles[1]}.csv", BWD_COLS,
+               dict(test="correctness", B=B_, H=H_, N=N_, D=D_, sigma=case.sigma,
+                    relerr_O=f"{rels[0]:.3e}", relerr_dQ=f"{rels[1]:.3e}", relerr_dK=f"{rels[2]:.3e}",
+                    relerr_dV=f"{rels[3]:.3e}", result="PASS" if max(rels) <= REL else "FAIL"))
     del ref
     B, H = q.shape[:2]
     picks = [(0, 0), (B - 1, H - 1)][:oracle_heads]
@@ -82,7 +89,7 @@ def inputs(shape, seed, sigma=1.0, dtype=torch.float16):
 def test_reference_backward_suite_fp16(case):
     q, k, v, do = (dev(x, torch.float16) for x in cases.make_bwd_inputs(case))
     log(f"bwd-suite {case.id}")
-    check_grads(q, k, v, do, (64, 64), f"bwd {case.id}", unit_variance=case.sigma == 1.0)
+    check_grads(q, k, v, do, (64, 64), f"bwd {case.id}", unit_variance=case.sigma == 1.0, case=case)
 
 
 @pytest.mark.parametrize("dt", list(DTYPES))

@@ -8,6 +8,7 @@ Cases:
 """
 
 import math
+import time
 
 import numpy as np
 import pytest
@@ -61,9 +62,11 @@ def test_reference_suite_fp16(case, tiles):
     is not a multiple of a tile runs with a partial last tile, where the reference rejects it)."""
     q, k, v = (dev(x, torch.float16) for x in cases.make_inputs(case))
     log(f"suite {case.id} tiles={tiles}")
+    t0 = time.perf_counter()
     o = fused_attention(q, k, v, *tiles)
     torch.cuda.synchronize()
-    check_forward(o, q, k, v, rows_count=24, label=f"{case.id} {tiles}")
+    seconds = time.perf_counter() - t0
+    check_forward(o, q, k, v, rows_count=24, label=f"{case.id} {tiles}", case=case, tiles=tiles, seconds=seconds)
 
 
 @pytest.mark.parametrize("case", [c for c in cases.all_cases() if c.N <= 2048][::3], ids=lambda c: c.id)

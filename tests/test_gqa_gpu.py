@@ -1,11 +1,13 @@
 """GPU parity of the fused causal GQA/MQA forward.
 
 Cases:
-  * the reference's 96-case GQA suite (tests/gqa/cases_gqa.py), fp16, tiles 64x64 and 128x128;
+  * the reference's 96-case GQA suite (tests/gqa/cases_gqa.py), fp16, at each tile config;
   * full-size GQA: B=2, H=32, H_kv=8, S=8192, D=128 bf16;
   * full-size MQA: B=1, H=32, H_kv=1, S=16384, D=64 fp16, inputs N(0,1) * 0.5;
   * H_kv == H must reproduce the MHA kernel's output bit for bit.
 """
+
+import time
 
 import numpy as np
 import pytest
@@ -19,15 +21,17 @@ from tests.gpu_util import check_forward, dev, log
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("tiles", [(64, 64), (128, 128)], ids=lambda t: f"{t[0]}x{t[1]}")
+@pytest.mark.parametrize("tiles", [(64, 64), (64, 128), (128, 64), (128, 128)], ids=lambda t: f"{t[0]}x{t[1]}")
 @pytest.mark.parametrize("case", cases.all_gqa_cases(), ids=lambda c: c.id)
 def test_reference_gqa_suite_fp16(case, tiles):
     q, k, v = (dev(x, torch.float16) for x in cases.make_gqa_inputs(case))
     assert k.shape[1] == case.H_kv  # never pre-expanded
     log(f"gqa-suite {case.id} tiles={tiles}")
+    t0 = time.perf_counter()
     o = fused_gqa_attention(q, k, v, *tiles)
     torch.cuda.synchronize()
-    check_forward(o, q, k, v, rows_count=24, label=f"{case.id} {tiles}")
+    seconds = time.perf_counter() - t0
+    check_forward(o, q, k, v, rows_count=24, label=f"{case.id} {tiles}", case=case, tiles=tiles, seconds=seconds)
 
 
 @pytest.mark.parametrize("tiles", [(64, 64), (128, 64)], ids=lambda t: f"{t[0]}x{t[1]}")
