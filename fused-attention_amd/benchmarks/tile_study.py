@@ -77,6 +77,25 @@ def variants(groups):
             out.append(("dkdv", f"cfg2-bwd split {ns}", CFG2, "bwd", dict(bm=128, bn=64, nsplit=ns), ""))
         for ns in (1, 16):
             out.append(("dkdv", f"mha-few-bwd split {ns}", MHA_FEW, "bwd", dict(bm=128, bn=64, nsplit=ns), ""))
+    if "rules" in groups:  # the shapes behind the dispatch rules' thresholds
+        for D in (128, 64, 32):
+            for gh in (2, 4):
+                out.append(("rules", f"gqa-few D={D} heads/wg {gh}", (2, 8, 1, 8192, D, "fp16"), "fwd",
+                            dict(bm=64, bn=64, gh=gh), ""))
+        for gh in (2, 4):
+            out.append(("rules", f"gqa-small heads/wg {gh}", (1, 16, 4, 4096, 128, "bf16"), "fwd",
+                        dict(bm=64, bn=64, gh=gh), ""))
+        for D in (32,):
+            for bm in (64, 128):
+                out.append(("rules", f"bwd D={D} dQ rows {bm} keys 64", (4, 32, 32, 4096, D, "bf16"), "bwd",
+                            dict(bm=bm, bn=64, nsplit=1), ""))
+        for wl, splits in (((1, 32, 1, 16384, 64, "fp16"), (4, 8, 16, 32)),
+                           ((1, 8, 1, 16384, 128, "bf16"), (4, 8, 16, 32)),
+                           ((1, 32, 4, 8192, 128, "bf16"), (1, 2, 4, 8)),
+                           ((1, 8, 8, 4096, 128, "bf16"), (1, 2, 4))):
+            for ns in splits:
+                out.append(("rules", "split {} B{} H{} Hkv{} S{} D{}".format(ns, *wl[:5]), wl, "bwd",
+                            dict(bm=64, bn=64, nsplit=ns), ""))
     return out
 
 
@@ -117,7 +136,17 @@ def run_target(args):
     P = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)  # noqa: E731
     cache = {}
     stream = torch.cuda.current_stream()
-    for group, name, wl, kind, prm, _ in variants(args.groups.split(",")):
+    if args.warm_s > 0:  # settle the clocks with torch work (not this library's kernels)
+        import time
+        a = torch.randn(4096, 4096, device="cuda", dtype=torch.bfloat16)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < args.warm_s:
+            for _ in range(8):
+                a = (a @ a).clamp_(-1, 1)
+            torch.cuda.synchronize()
+        del a
+    todo = variants(args.groups.split(",")) * args.rounds
+    for group, name, wl, kind, prm, _ in todo:
         (q, k, v, o, do, lse, (dq, dk, dv)), pre = _inputs(torch, wl, cache)
         B, H, Hkv, S, D, dt = wl
         code_dt = _lib.dtype_code(q.dtype)
@@ -230,15 +259,18 @@ def profile(args):
     os.makedirs(args.out_dir, exist_ok=True)
     env = dict(os.environ)
     env.setdefault("TMPDIR", "/tmp")
-    child = [sys.executable, "-m", "benchmarks.tile_study", "--_target", "--groups", args.groups,
-             "--calls", str(args.calls)]
+    def child(calls, warm, rounds):
+        return [sys.executable, "-m", "benchmarks.tile_study", "--_target", "--groups", args.groups,
+                "--calls", str(calls), "--warm-s", str(warm), "--rounds", str(rounds)]
     results = {}
     manifest = None
     commands = []
     for name, extra in PASSES:
         d = os.path.join(args.out_dir, name)
+        timed = name == "trace"   # the timing pass warms the clocks first and takes more calls
         cmd = ["timeout", "-s", "KILL", str(args.pass_timeout), "rocprofv3", *extra, "--output-format", "csv",
-               "-d", d, "-o", name, "--", *child]
+               "-d", d, "-o", name, "--",
+               *child(args.calls if timed else 2, args.warm_s if timed else 0, args.rounds if timed else 1)]
         commands.append(" ".join(cmd))
         print(f"[tile_study] pass {name}: {' '.join(extra)}", flush=True)
         log = os.path.join(args.out_dir, f"{name}.log")
@@ -246,7 +278,7 @@ def profile(args):
             r = subprocess.run(cmd, cwd=PKG_ROOT, env=env, stdout=f, stderr=subprocess.STDOUT, text=True)
         with open(log) as f:
             man = [json.loads(ln[8:]) for ln in f.read().splitlines() if ln.startswith("VARIANT ")]
-        if r.returncode != 0 and len(man) != len(variants(args.groups.split(","))):
+        if r.returncode != 0 and len(man) != len(variants(args.groups.split(","))) * (args.rounds if timed else 1):
             sys.exit(f"pass {name} failed (rc {r.returncode}); see {args.out_dir}/{name}.log")
         manifest = man
         csv_name = "kernel_trace" if name == "trace" else "counter_collection"
@@ -256,16 +288,21 @@ def profile(args):
             if not found:
                 sys.exit(f"pass {name}: no {csv_name}.csv under {d}")
             path = found[0]
-        results[name] = split_by_variant(fa_dispatches(path), manifest)
+        # per variant name: every call of every round, in order
+        per_name = {}
+        for m, calls in zip(manifest, split_by_variant(fa_dispatches(path), manifest)):
+            per_name.setdefault(m["name"], []).append(calls)
+        results[name] = per_name
     rows = []
-    for vi, (group, vname, wl, kind, prm, _) in enumerate(variants(args.groups.split(","))):
-        trace_calls = results["trace"][vi]
-        last = {k: results[k][vi][-1] for k in ("pmc1", "pmc2")}
-        for pos in range(len(trace_calls[-1])):
-            _, rec = trace_calls[-1][pos]
+    for group, vname, wl, kind, prm, _ in variants(args.groups.split(",")):
+        rounds = results["trace"][vname]           # [round][call][dispatch]
+        last = {k: results[k][vname][-1][-1] for k in ("pmc1", "pmc2")}
+        for pos in range(len(rounds[-1][-1])):
+            _, rec = rounds[-1][-1][pos]
             kern = short_kernel(rec["name"])
+            # every call but the first of each round
             durs = [(int(c[pos][1]["row"]["End_Timestamp"]) - int(c[pos][1]["row"]["Start_Timestamp"])) / 1e3
-                    for c in trace_calls[1:] or trace_calls]
+                    for calls in rounds for c in (calls[1:] or calls)]
             us = statistics.median(durs)
             flops, nbytes = kernel_flops_bytes(kern, wl)
             counters = {}
@@ -308,7 +345,12 @@ def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--out-dir", default=os.path.join(os.path.dirname(PKG_ROOT), "gpurun_out", "tile_study"))
     p.add_argument("--groups", default="fwd,gqa,dq,dkdv")
-    p.add_argument("--calls", type=int, default=3, help="calls per variant (the last one's counters are kept)")
+    p.add_argument("--rounds", type=int, default=3,
+                   help="passes over all variants in the timing pass (interleaves them in time)")
+    p.add_argument("--calls", type=int, default=8,
+                   help="calls per variant and round in the timing pass (median over all calls but the "
+                        "first of each round); the counter passes make 2 and keep the last one's counters")
+    p.add_argument("--warm-s", type=float, default=2.0, help="seconds of untimed GPU work before the timing pass")
     p.add_argument("--pass-timeout", type=int, default=240)
     p.add_argument("--_target", dest="target", action="store_true", help=argparse.SUPPRESS)
     return p.parse_args(argv)

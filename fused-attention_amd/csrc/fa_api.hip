@@ -5,6 +5,7 @@
 // attention/backward/fused_backward.py:151-158); the Python layer raises the
 // reference's exception types before it ever reaches this ABI, so these
 // checks are the last line of defence for C callers.
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 #include <mutex>
@@ -47,6 +48,9 @@ fa::BwdFn bwd_table(int dtype, int D, int bm, int bn) {
 // as fit in 8 waves (512 threads), each head taking block_m/32 waves.  With
 // 128-key tiles a wave holds two 128-key score tiles in flight and needs more
 // than the 256 VGPRs of two waves per SIMD, so the workgroup stays at 4 waves.
+// Counters (profiles/tile_study_mha_gqa_bwd.md, GQA B=2 H=32 H_kv=8 S=8192 D=128):
+// one head of 64 rows 813 TFLOP/s, MFMA busy 43.0 %; two heads 1112 / 61.7 %; four
+// heads 1122 / 56.4 %.
 int heads_per_wg(int group, int block_m, int block_n) {
   int cap = (block_n == 128 ? 128 : 256) / block_m;  // waves / (block_m / 32)
   if (cap > kMaxGroupHeadsPerWg) cap = kMaxGroupHeadsPerWg;
@@ -93,7 +97,10 @@ int cu_count() {
 // workgroups per CU, where the heavy-first order cannot balance the causal
 // triangle (B=2 H=8 H_kv=1 S=8192 fp16, tile 64x64: D=128 0.328 -> 0.288 ms,
 // D=32 0.175 -> 0.123 ms; at B=2 H=32 H_kv=8, 2048 workgroups, four stay 3 %
-// faster).  Two heads of 64 rows still hold two waves per SIMD.
+// faster).  Two heads of 64 rows still hold two waves per SIMD.  With the heavy-first
+// order of today's kernel (profiles/tile_study_mha_gqa_bwd.md): B=1 H=16 H_kv=4 S=4096
+// D=128 two heads 737 TFLOP/s, four 619; B=2 H=8 H_kv=1 S=8192 D=32 559 vs 532, and
+// equal at D=64 and D=128.
 int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
   int gh = heads_per_wg(group, block_m, block_n);
   if (gh == 4 && (long long)B * (H / 4) * ((S + block_m - 1) / block_m) < 4LL * cu_count()) gh = 2;
@@ -108,15 +115,25 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
 // Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows: tile_n = 64:
 // D=128 685 -> 970, D=64 582 -> 809, D=32 358 -> 552; tile_n = 128: D=128 350 -> 637
 // (D <= 64 about equal, so left).  dQ: D = 128 only (both tile_n).
+// Counters (profiles/tile_study_mha_gqa_bwd.md, B=4 H=32 S=4096 bf16): 64 rows x 64 keys at
+// D=128 run 707 TFLOP/s with MFMA busy 36.8 % (one wave per SIMD), 128 rows 907 / 54.8 %.
+// dQ: 64 -> 128 rows at D=128 849 -> 1121 TFLOP/s (MFMA busy 42.6 -> 59.2 %); at D=64 920 -> 968
+// with 64-key tiles and 683 -> 972 with 128-key tiles; at D=32 703 -> 717.
 int fwd_block_m(int block_m, int block_n, int D, int gh) {
   return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
 }
-int dq_block_m(int block_m, int D) { return (block_m == 64 && D == 128) ? 128 : block_m; }
+int dq_block_m(int block_m, int D) { return (block_m == 64 && D >= 64) ? 128 : block_m; }
 
-// Workgroups the dK/dV kernel should have for its heavy-first order to balance:
-// two rounds of one workgroup per CU (a split costs an fp32 partial write, read
-// and reduction, so it is kept to what load balance needs).
-int dkdv_target_workgroups() { return 2 * cu_count(); }
+// Workgroups the dK/dV kernel should have for its heavy-first order to balance: two
+// rounds of one workgroup per CU up to S = 4096, and one round more per 4096 keys
+// beyond, since the heaviest key tile's pairs grow with S while the average does not
+// keep up (a split costs an fp32 partial write, read and reduction, so it is kept to
+// what load balance needs).  Measured (profiles/tile_study_mha_gqa_bwd.md, dK/dV +
+// reduction): MQA B=1 H=32 S=16384 D=64, split 4 / 8 / 16 / 32: 3158 / 2215 / 2087 /
+// 2128 us; B=1 H=8 H_kv=1 S=16384 D=128, 4 / 8 / 16: 1457 / 1088 / 1122; GQA B=1 H=32
+// H_kv=4 S=8192 D=128, 2 / 4 / 8: 1115 / 1103 / 1142; MHA B=1 H=8 S=4096 D=128, 1 / 2 /
+// 4: 114 / 95 / 120; the headline B=4 H=32 S=4096: 1 / 2: 1304 / 1708.
+int dkdv_target_workgroups(int S) { return 2 * cu_count() * std::max(1, (S + 4095) / 4096); }
 
 size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
   return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
@@ -139,7 +156,7 @@ constexpr int kMaxDkdvSplit = 64;
 constexpr int kMinSplitPairs = 64;
 int dkdv_nsplit(int B, int H, int H_kv, int S) {
   const long long items = (long long)B * H_kv * ((S + fa::kDkdvKeys - 1) / fa::kDkdvKeys);
-  const long long want = dkdv_target_workgroups();
+  const long long want = dkdv_target_workgroups(S);
   const long long pairs = (long long)(H / H_kv) * ((S + 63) / 64);
   if (items >= want || pairs < kMinSplitPairs) return 1;
   long long s = (want + items - 1) / items;
