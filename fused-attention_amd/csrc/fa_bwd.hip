@@ -648,16 +648,19 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   const int c = lane & 31, hh = lane >> 5;
 
   // work item: (b, h, query tile), XCD aware as the forward: XCD wg % 8 takes a
-  // contiguous range of (b, h) and dispatches the heaviest query tiles of all of
-  // them first (1.4 % faster than one (b, h) after another at B=4 H=32 S=4096 D=128)
+  // contiguous range of (b, h) and walks them in groups of xcd_group() heads, heaviest
+  // query tiles of the group first (at B=4 H=32 S=4096 D=128, against all 16 heads of
+  // the XCD at once: one (b, h) after another -1.4 %, groups of 4 +1.5 %)
   const int nq = (S + BM - 1) / BM;
   const int nunits = B * H;
   const int wg = blockIdx.x;
   int bh, qt;
   if (nunits % 8 == 0) {
     const int per = nunits / 8, i = wg / 8;
-    bh = (wg % 8) * per + i % per;
-    qt = nq - 1 - i / per;
+    const int G = xcd_group(per, nq);
+    const int grp = i / (G * nq), r = i % (G * nq);
+    bh = (wg % 8) * per + grp * G + r % G;
+    qt = nq - 1 - r / G;
   } else {
     bh = wg % nunits;
     qt = nq - 1 - wg / nunits;

@@ -151,6 +151,16 @@ __device__ __forceinline__ float quad_sum(float x) {
   return x;
 }
 
+// Units (heads, or head groups) an XCD works on at one time when its workgroups walk
+// `per` units of `nq` query tiles each: about 256 workgroups per group (4 rounds of an
+// XCD's 32 CUs x 2 resident workgroups), as a power of two dividing `per`.
+__device__ __forceinline__ int xcd_group(int per, int nq) {
+  const int want = 256 / nq;
+  int g = 1;
+  while (2 * g <= want && per % (2 * g) == 0) g *= 2;
+  return g;
+}
+
 __device__ __forceinline__ u32x4 lds_read16(const unsigned char* base, int byte_off) {
   return *reinterpret_cast<const u32x4*>(base + byte_off);
 }
