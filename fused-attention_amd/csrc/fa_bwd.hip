@@ -18,6 +18,10 @@
 //                dV^T += dO^T P and dK^T += Q^T dS, reading dO^T and Q^T with
 //                ds_read_b64_tr_b16.  At D >= 64 the full tiles run a hand-pipelined
 //                schedule (operand reads a region ahead of their MFMAs).
+//   dkdv_pair_kernel: the same work at D = 128 when the per-row terms are handed
+//                over, each 32-key block split over two waves by role (S, P and
+//                dV / dP, dS and dK, P passed through LDS), so two waves share
+//                every SIMD where dkdv_kernel fits one.
 //   dkdv_reduce_kernel: only with a caller workspace, when B * H_kv key tiles alone
 //                would leave the GPU idle (MQA, few heads): each key tile's pairs are
 //                then split over several dK/dV workgroups that write fp32 partial
@@ -41,6 +45,7 @@
 // distinct 16-byte slots of the 256-byte bank line, and 4 consecutive rows read
 // as one 32-byte piece (a transposed read) land on 4 distinct 32-byte groups.
 #include <algorithm>
+#include <type_traits>
 
 #include "fa_device.h"
 #include "fa_launch.h"
@@ -51,6 +56,12 @@ typedef short i16x4b __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4b lds_i16x4b;
 
 constexpr int kBwdWaitVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0)
+
+// dK / dV at D = 128 with the row terms handed over: paired waves (1) or one wave
+// per 32-key block (0)
+#ifndef FA_DKDV_PAIR
+#define FA_DKDV_PAIR 1
+#endif
 
 template <bool B>
 struct BTag {
@@ -614,6 +625,472 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 }
 
 // ===========================================================================
+// dK / dV with paired waves (D = 128, per-row terms handed over)
+// ===========================================================================
+// The work items, pair sequence and DMA of dkdv_kernel<..., RB = true>, with
+// each 32-key block split over two waves by role instead of one wave holding
+// everything:
+//   role 0 keeps the K rows and dV:  S = Q_b K^T - LSE/c,  P = exp2(c S),
+//          dV^T += dO^T P;  it leaves P in LDS for its partner as fp16 (P lies
+//          in [0, 1]: fp16's 11-bit significand keeps the rounding of P 8x below
+//          bf16's, and fp32 slots would not fit beside the three tile buffers)
+//   role 1 keeps the V rows and dK:  dP = dO_b V^T - Delta,  dS = P dP,
+//          dK^T += Q^T dS, with P read back from LDS.
+// Each wave needs about half the registers of a dkdv_kernel wave (one K or V
+// row set and one accumulator instead of two of each), so two waves share every
+// SIMD, one of each role, and each one's LDS and MFMA latencies run under the
+// other's work; dkdv_kernel at D = 128 holds one wave per SIMD.  The roles run
+// a pair apart in one loop with one barrier per pair: in iteration t role 0
+// forms S and P of pair t+1, then adds pair t to dV (P(t) kept packed in
+// registers); role 1 adds pair t to dK (P(t) from LDS, dP(t) kept from the
+// previous iteration), then forms dP of pair t+1.  Each SIMD thus mixes the
+// full-rate operand reads of one product with the transposed reads of the
+// other throughout the iteration.  P of pair t sits in slot t % 2.
+template <typename E, int D, int BMQ, int BNK>
+__global__ __launch_bounds__(4 * BNK)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
+void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                      const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
+                      const float* __restrict__ Rb, uint16_t* __restrict__ dK, uint16_t* __restrict__ dV,
+                      float* __restrict__ Pk, float* __restrict__ Pv, int nsplit,
+                      int B, int H, int Hkv, int S, float scale_log2, float sm_scale) {
+  static_assert(BMQ == 64, "a query tile is two 32-row blocks");
+  constexpr int NKB = BNK / 32;                          // key blocks = wave pairs
+  constexpr int NW = 2 * NKB;
+  constexpr int KT = D / 16, DB = D / 32;
+  constexpr int ROWB = D * 2, CPR = ROWB / 16;
+  constexpr int TILE = BMQ * ROWB;                       // bytes of one Q / dO tile
+  constexpr int NBLK = TILE / 1024;
+  constexpr int OFF_L = 2 * TILE;                        // Q | dO | -LSE/c | -Delta
+  constexpr int BUFA = (OFF_L + 2 * BMQ * 4 + 1023) / 1024 * 1024;
+  constexpr int NBUF = 3;
+  constexpr int NDMA = (NBLK + NW - 1) / NW;
+  constexpr int XPS = NKB * 2 * 2 * 64;                  // 16-byte P pieces per slot
+  static_assert(TILE % 1024 == 0 && NBLK % NW == 0, "tiles are whole 1 KB DMA blocks, split evenly");
+  const float NEG_INF = -__builtin_inff();
+
+  __shared__ __attribute__((aligned(1024))) unsigned char bufs[NBUF * BUFA];
+  // the P handed over: fp16 pairs (the same words as the dV operand for fp16 input)
+  constexpr bool PF16 = std::is_same<E, F16>::value;
+  // packed P, two slots: piece (query block qb, k-step half i1) of lane L of key
+  // block kb at [slot][kb][qb][i1][L] (each wave's 16-byte write or read is 1 KB
+  // contiguous)
+  __shared__ __attribute__((aligned(16))) u32x4 xp[2 * XPS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int role = wave / NKB, kb = wave % NKB;
+  const int c = lane & 31, hh = lane >> 5;
+
+  // work item: as in dkdv_kernel
+  const int G = H / Hkv;
+  const int nk = (S + BNK - 1) / BNK;
+  const int total = B * Hkv * nsplit * nk;
+  const int wg = blockIdx.x;
+  const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
+  const int u = L / nk, jt = L % nk;
+  const int bkv = u / nsplit;
+  const size_t base = (size_t)bkv * S * D;
+  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;
+
+  const int k0w = jt * BNK + 32 * kb;     // first key of this wave's block
+  const int n = k0w + c;                  // this lane's key
+  const bool active = k0w < S;            // wave-uniform
+
+  // K (role 0) or V (role 1) rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
+  u32x4 xf[KT];
+  if (active) {
+    const uint16_t* xr = (role ? V : K) + base + (size_t)min(n, S - 1) * D + 8 * hh;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) xf[t] = gload16(xr + 16 * t);
+  }
+
+  const int nq = (S + BMQ - 1) / BMQ;
+  const int i0 = (jt * BNK) / BMQ;
+  const int NI = nq - i0;
+  const int T = G * NI;
+  const int hc = u % nsplit;
+  const int tb = (int)((long long)T * hc / nsplit), te = (int)((long long)T * (hc + 1) / nsplit);
+
+  // DMA of pair (di, dg)'s Q and dO tiles and its two row-term slices: every wave
+  // copies NDMA 1 KB blocks of each tile, waves 0 and 1 one slice each
+  const int drow = lane / CPR, dch = lane % CPR;
+  int dvo[NDMA];
+#pragma unroll
+  for (int x = 0; x < NDMA; ++x) {
+    const int row = (wave + x * NW) * (1024 / ROWB) + drow;
+    dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
+  }
+  auto bufp = [&](int t) __attribute__((always_inline)) {
+    return bufs + __builtin_amdgcn_readfirstlane((t % NBUF) * BUFA);
+  };
+  int di = i0 + tb / G, dg = tb % G;
+  // the next pair's descriptors (advancing the sequence), and its DMA in
+  // 2 NDMA + 1 parts: part 2x / 2x+1 = block x of the Q / dO tile, part 2 NDMA =
+  // the row-term slice (waves 0 and 1)
+  struct Dma {
+    __amdgpu_buffer_rsrc_t q, d, r;
+    unsigned char* buf;
+  };
+  auto dma_prep = [&](unsigned char* buf) __attribute__((always_inline)) {
+    const size_t row0 = (size_t)(bh0 + dg) * S + (size_t)di * BMQ;
+    const int rows = min(BMQ, S - di * BMQ);
+    Dma j{make_rsrc(Q + row0 * D, rows * ROWB), make_rsrc(dO + row0 * D, rows * ROWB),
+          make_rsrc(Rb + (wave == 1 ? (size_t)B * H * S : 0) + row0, rows * 4), buf};
+    if (++dg == G) {
+      dg = 0;
+      ++di;
+    }
+    return j;
+  };
+  auto dma_part = [&](const Dma& j, int k) __attribute__((always_inline)) {
+    if (k < 2 * NDMA) {
+      const int blk = wave + (k >> 1) * NW;
+      dma16((k & 1) ? j.d : j.q, j.buf + (k & 1) * TILE + blk * 1024, dvo[k >> 1], 0);
+    } else if (wave < 2) {
+      dma4(j.r, j.buf + OFF_L + wave * 4 * BMQ, 4 * lane, 0);
+    }
+  };
+  auto dma_next = [&](unsigned char* buf) __attribute__((always_inline)) {
+    const Dma j = dma_prep(buf);
+#pragma unroll
+    for (int k = 0; k <= 2 * NDMA; ++k) dma_part(j, k);
+  };
+
+  TileOffsets<ROWB> to;
+  to.init(lane);
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+
+  const int a1 = role ? TILE : 0;               // S / dP A rows: Q or dO
+  const int a2 = role ? 0 : TILE;               // dV / dK A^T rows: dO or Q
+  const int lo = OFF_L + role * 4 * BMQ;        // -LSE/c or -Delta
+  auto slot = [&](int t, int qb, int i1) __attribute__((always_inline)) {
+    return xp + (t & 1) * XPS + ((kb * 2 + qb) * 2 + i1) * 64 + lane;
+  };
+
+  auto load_rows = [&](const float* src, int qb) __attribute__((always_inline)) {
+    f32x16 v;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(src + 32 * qb + 8 * gq + 4 * hh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * gq + e] = x[e];
+    }
+    return v;
+  };
+  // query block qb of pair t meets this wave's keys (wave-uniform)
+  auto live = [&](int t, int qb) __attribute__((always_inline)) {
+    return active && (i0 + t / G) * BMQ + 32 * qb + 31 >= k0w;
+  };
+
+  // front(t): S - LSE/c (role 0) or dP - Delta (role 1) of pair t's two query
+  // blocks, the blocks' MFMA chains interleaved; role 0 turns S into P (keys past
+  // the query masked on the diagonal block), keeps it packed in pk and writes it to
+  // slot t % 2.  FULL: pair t lies wholly past this wave's keys (no test, no mask).
+  auto front = [&](int t, f32x16 (&x)[2], u32x4 (&pk)[2][2], auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    const unsigned char* buf = bufp(t);
+    const int qrow0 = (i0 + t / G) * BMQ;
+    const bool l0 = FULL || live(t, 0), l1 = FULL || live(t, 1);
+    if (!l1) return;  // (l0 implies l1)
+    x[1] = load_rows(reinterpret_cast<const float*>(buf + lo), 1);
+    if (l0) {
+      x[0] = load_rows(reinterpret_cast<const float*>(buf + lo), 0);
+#pragma unroll
+      for (int t2 = 0; t2 < KT; ++t2) {
+        x[0] = mfma32<E>(lds_read16(buf + a1, to.opnd[t2]), xf[t2], x[0]);
+        x[1] = mfma32<E>(lds_read16(buf + a1, to.opnd[t2] + 32 * ROWB), xf[t2], x[1]);
+      }
+    } else {
+#pragma unroll
+      for (int t2 = 0; t2 < KT; ++t2)
+        x[1] = mfma32<E>(lds_read16(buf + a1, to.opnd[t2] + 32 * ROWB), xf[t2], x[1]);
+    }
+    if (role != 0) return;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if (qb == 0 && !l0) continue;
+      const bool diag = !FULL && qrow0 + 32 * qb == k0w;
+      float p[16];
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        float v = x[qb][g];
+        if (diag && c > acc_row(g, hh)) v = NEG_INF;
+        p[g] = fast_exp2(v * scale_log2);
+      }
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+        u32x4 h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          pk[qb][i1][q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+          h[q] = PF16 ? pk[qb][i1][q] : pack2<F16>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+        }
+        *slot(t, qb, i1) = h;
+      }
+    }
+  };
+  // back(t): dV^T += dO^T P (role 0, P from pk) or dK^T += Q^T dS with
+  // dS = P (dP - Delta) (role 1, P from slot t % 2, dP - Delta from x); k-slots:
+  // queries 32qb + 16i1 + 8r2 + 4hh + 0..3
+  auto back = [&](int t, const f32x16 (&x)[2], const u32x4 (&pk)[2][2], auto full) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full)::value;
+    const unsigned char* buf = bufp(t);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      if (!FULL && !live(t, qb)) continue;
+      u32x4 bop[2];
+      if (role == 0) {
+        bop[0] = pk[qb][0];
+        bop[1] = pk[qb][1];
+      } else {
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const u32x4 w = *slot(t, qb, i1);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int g = 8 * i1 + 2 * q;
+            bop[i1][q] = pack2<E>(to_f32<F16>(w[q] & 0xffffu) * x[qb][g], to_f32<F16>(w[q] >> 16) * x[qb][g + 1]);
+          }
+        }
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const int uu = 2 * qb + i1;
+          acc[db] = mfma32<E>(tr_read2(buf + a2, to.tr(db, uu, 0), to.tr(db, uu, 1)), bop[i1], acc[db]);
+        }
+    }
+  };
+
+  // pairs before TE meet this workgroup's keys (edge tests, the diagonal mask);
+  // the rest lie wholly past them.  Only the last key tile can have inactive waves,
+  // and it meets at most two query tiles (NI <= 2), so the full paths need no
+  // activity test.
+  const int TE = G * min(2, NI);
+  // pair t+1 has landed, P(t) is visible, and nobody reads pair t-1's buffer or
+  // slot (t+1) % 2 any more
+  auto sync = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    __syncthreads();
+  };
+  auto top = [&](int t) __attribute__((always_inline)) {
+    sync();
+    if (t + 2 < te) dma_next(bufp(t + 2));
+  };
+  f32x16 x[2];
+  u32x4 pk[2][2], pkn[2][2];
+  if (tb < te) {  // (a chunk of a light key tile can be empty: it stores zeros)
+    dma_next(bufp(tb));
+    if (tb + 1 < te) dma_next(bufp(tb + 1));
+    // pair tb has landed once at most pair tb+1's operations are outstanding
+    if (tb + 1 < te) {
+      if (wave < 2) __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA + 1));
+      else __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA));
+    } else {
+      __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
+    }
+    __syncthreads();
+    if (tb >= TE) front(tb, x, pk, BTag<true>{});
+    else front(tb, x, pk, BTag<false>{});
+  }
+  // Full pairs with a next pair run as one stream of 32 MFMAs per wave, operand
+  // reads issued three MFMAs ahead (a rotating set of four, pinned by
+  // sched_barrier; left to itself the compiler issued each read just before its
+  // MFMA and waited on it):
+  //   role 0: S(t+1) (full-rate reads; both query blocks' chains interleaved),
+  //           then dV(t) (transposed reads), with P(t+1) formed, packed and
+  //           written to its slot under the dV MFMAs
+  //   role 1: dK(t) (transposed reads), with dS(t) formed from slot t % 2 and x
+  //           first, then dP(t+1) (full-rate reads) into x
+  // so the two waves of a SIMD read LDS at full and at half rate in turn.  A
+  // dV / dK MFMA j = 0..15 is (query block j / 8, d block (j / 2) % 4, k-step
+  // half j % 2), so every accumulator sees its products in the order back() adds
+  // them; an S / dP MFMA j is k-step j / 2 of query block j % 2.
+  auto rd_sd = [&](const unsigned char* buf, int j) __attribute__((always_inline)) {
+    return lds_read16(buf + a1, to.opnd[j >> 1] + 32 * (j & 1) * ROWB);
+  };
+  auto rd_w = [&](const unsigned char* buf, int j) __attribute__((always_inline)) {
+    const int qb = j >> 3, db = (j >> 1) & 3, i1 = j & 1;
+    return tr_read2(buf + a2, to.tr(db, 2 * qb + i1, 0), to.tr(db, 2 * qb + i1, 1));
+  };
+  // A stream also issues pair t+2's DMA, one part every other MFMA from the first,
+  // so the vector memory unit takes it in the background (issued together after
+  // the barrier, the eight waves' DMA stalled each of them by 300-500 cycles)
+  auto stream0 = [&](int t, const u32x4 (&cur)[2][2], u32x4 (&nxt)[2][2]) __attribute__((always_inline)) {
+    const bool dm = t + 2 < te;
+    Dma job;
+    if (dm) job = dma_prep(bufp(t + 2));
+    const unsigned char* bn = bufp(t + 1);
+    const unsigned char* bc = bufp(t);
+    x[0] = load_rows(reinterpret_cast<const float*>(bn + lo), 0);
+    x[1] = load_rows(reinterpret_cast<const float*>(bn + lo), 1);
+    auto rd = [&](int i) __attribute__((always_inline)) { return i < 16 ? rd_sd(bn, i) : rd_w(bc, i - 16); };
+    u32x4 hp[2][2];  // fp16 copy of P for the slot (bf16 input)
+    // P of query block qb, elements 4k .. 4k+3 (k = 0..3)
+    auto p_chunk = [&](int qb, int k) __attribute__((always_inline)) {
+      float p[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[e] = fast_exp2(x[qb][4 * k + e] * scale_log2);
+      const int i1 = k >> 1, q0 = 2 * (k & 1);
+      nxt[qb][i1][q0] = pack2<E>(p[0], p[1]);
+      nxt[qb][i1][q0 + 1] = pack2<E>(p[2], p[3]);
+      if constexpr (!PF16) {
+        hp[qb][i1][q0] = pack2<F16>(p[0], p[1]);
+        hp[qb][i1][q0 + 1] = pack2<F16>(p[2], p[3]);
+      }
+      if (k & 1) *slot(t + 1, qb, i1) = PF16 ? nxt[qb][i1] : hp[qb][i1];
+    };
+    constexpr int PD = 3;
+    u32x4 rot[PD + 1];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) rot[i] = rd(i);
+    static_for<0, 32>([&](auto I) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value;
+      if constexpr (i + PD < 32) rot[(i + PD) % (PD + 1)] = rd(i + PD);
+      if constexpr (i % 2 == 0 && i / 2 <= 2 * NDMA)
+        if (dm) dma_part(job, i / 2);
+      if constexpr (i < 16) {
+        x[i & 1] = mfma32<E>(rot[i % (PD + 1)], xf[i >> 1], x[i & 1]);
+      } else {
+        constexpr int j = i - 16, qb = j >> 3, db = (j >> 1) & 3, i1 = j & 1;
+        acc[db] = mfma32<E>(rot[i % (PD + 1)], cur[qb][i1], acc[db]);
+      }
+      // S of block 0 is complete after MFMA 14, of block 1 after 15
+      if constexpr (i >= 17 && i <= 23 && (i - 17) % 2 == 0) p_chunk(0, (i - 17) / 2);
+      if constexpr (i >= 25 && (i - 25) % 2 == 0) p_chunk(1, (i - 25) / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  auto stream1 = [&](int t) __attribute__((always_inline)) {
+    const bool dm = t + 2 < te;
+    Dma job;
+    if (dm) job = dma_prep(bufp(t + 2));
+    const unsigned char* bn = bufp(t + 1);
+    const unsigned char* bc = bufp(t);
+    u32x4 w[2][2], bop[2][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) w[qb][i1] = *slot(t, qb, i1);
+    auto rd = [&](int i) __attribute__((always_inline)) { return i < 16 ? rd_w(bc, i) : rd_sd(bn, i - 16); };
+    // dS of query block qb, elements 4k .. 4k+3
+    auto ds_chunk = [&](int qb, int k) __attribute__((always_inline)) {
+      const int i1 = k >> 1, q0 = 2 * (k & 1);
+#pragma unroll
+      for (int q = q0; q < q0 + 2; ++q) {
+        const int g = 8 * i1 + 2 * q;
+        const uint32_t v = w[qb][i1][q];
+        bop[qb][i1][q] = pack2<E>(to_f32<F16>(v & 0xffffu) * x[qb][g], to_f32<F16>(v >> 16) * x[qb][g + 1]);
+      }
+    };
+    constexpr int PD = 3;
+    u32x4 rot[PD + 1];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) rot[i] = rd(i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ds_chunk(0, k);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, 32>([&](auto I) __attribute__((always_inline)) {
+      constexpr int i = decltype(I)::value;
+      if constexpr (i + PD < 32) rot[(i + PD) % (PD + 1)] = rd(i + PD);
+      if constexpr (i % 2 == 0 && i / 2 <= 2 * NDMA)
+        if (dm) dma_part(job, i / 2);
+      if constexpr (i < 4) ds_chunk(1, i);
+      if constexpr (i == 8) {  // dS is formed: x takes dP(t+1) - Delta
+        x[0] = load_rows(reinterpret_cast<const float*>(bn + lo), 0);
+        x[1] = load_rows(reinterpret_cast<const float*>(bn + lo), 1);
+      }
+      if constexpr (i < 16) {
+        constexpr int qb = i >> 3, db = (i >> 1) & 3, i1 = i & 1;
+        acc[db] = mfma32<E>(rot[i % (PD + 1)], bop[qb][i1], acc[db]);
+      } else {
+        constexpr int j = i - 16;
+        x[j & 1] = mfma32<E>(rot[i % (PD + 1)], xf[j >> 1], x[j & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // The two roles run separate loops with the same barriers, so each keeps only its
+  // own state in registers.  Role 0 alternates the two packed-P register sets by
+  // unrolling two pairs.
+  int t = tb;
+  if (role == 0) {
+    auto step = [&](int t, u32x4 (&cur)[2][2], u32x4 (&nxt)[2][2], auto full) __attribute__((always_inline)) {
+      top(t);
+      if (t + 1 < te) front(t + 1, x, nxt, full);
+      back(t, x, cur, full);
+    };
+    for (; t < min(te, TE); ++t) {  // edge pairs: at most two per K/V head
+      step(t, pk, pkn, BTag<false>{});
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
+    }
+    for (; t + 2 < te; t += 2) {
+      sync();
+      stream0(t, pk, pkn);
+      sync();
+      stream0(t + 1, pkn, pk);
+    }
+    for (; t < te; ++t) {
+      step(t, pk, pkn, BTag<true>{});
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
+    }
+  } else {
+    for (; t < min(te, TE); ++t) {
+      top(t);
+      back(t, x, pk, BTag<false>{});
+      if (t + 1 < te) front(t + 1, x, pkn, BTag<false>{});
+    }
+    for (; t + 1 < te; ++t) {
+      sync();
+      stream1(t);
+    }
+    for (; t < te; ++t) {
+      top(t);
+      back(t, x, pk, BTag<true>{});
+      if (t + 1 < te) front(t + 1, x, pkn, BTag<true>{});
+    }
+  }
+
+  // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7; role 0 stores
+  // dV, role 1 dK
+  if (!active || n >= S) return;
+  const float mul = role ? sm_scale : 1.0f;
+  if (nsplit > 1) {  // fp32 partial sums of this chunk, dK already scaled
+    float* pr = (role ? Pk : Pv) + ((size_t)u * S + n) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) {
+        const int d0 = db * 32 + 16 * i1 + 8 * hh;
+#pragma unroll
+        for (int h4 = 0; h4 < 2; ++h4) {
+          const int g0 = 8 * i1 + 4 * h4;
+          gstore_f32x4(pr + d0 + 4 * h4, f32x4{acc[db][g0] * mul, acc[db][g0 + 1] * mul,
+                                               acc[db][g0 + 2] * mul, acc[db][g0 + 3] * mul});
+        }
+      }
+    return;
+  }
+  uint16_t* r = (role ? dK : dV) + base + (size_t)n * D;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i1 = 0; i1 < 2; ++i1) gstore16(r + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, mul));
+}
+
+// ===========================================================================
 // dQ
 // ===========================================================================
 // Waves per SIMD the dQ kernel is register-budgeted for: two whenever two
@@ -965,12 +1442,22 @@ static bool launch_dkdv(const BwdArgs& a) {
   static_assert(BNK == kDkdvKeys, "host split heuristics assume this key tile");
   const int nsplit = a.nsplit > 1 ? a.nsplit : 1;
   const dim3 grid(a.B * a.Hkv * nsplit * ((a.S + BNK - 1) / BNK)), block(2 * BNK);
-  if (a.rowb)
+  bool paired = false;
+  if constexpr (FA_DKDV_PAIR && D == 128) {
+    if (a.rowb) {
+      hipLaunchKernelGGL((dkdv_pair_kernel<E, D, BMQ, BNK>), grid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
+                         (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.d_o,
+                         a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,
+                         nsplit, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
+      paired = true;
+    }
+  }
+  if (!paired && a.rowb)
     hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK, true>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.o,
                        (const uint16_t*)a.d_o, a.lse, a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,
                        nsplit, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);
-  else
+  else if (!paired)
     hipLaunchKernelGGL((dkdv_kernel<E, D, BMQ, BNK, false>), grid, block, 0, (hipStream_t)a.stream,
                        (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.o,
                        (const uint16_t*)a.d_o, a.lse, nullptr, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,

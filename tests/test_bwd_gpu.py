@@ -196,7 +196,8 @@ def _fa_bwd_no_workspace(q, k, v, do, tiles):
 def test_reference_entry_without_workspace(shape, dt, tiles):
     """fa_bwd (dK/dV then dQ, Delta formed in both) against the fp32 reference at the max-abs bar,
     and against the Python path (dQ first, dK/dV reading the per-row terms): dQ bitwise equal,
-    dK/dV equal up to the fp32 summation order of Delta."""
+    dK/dV equal up to the fp32 summation order of Delta and, at D = 128, dS formed from P
+    rounded to fp16."""
     q, k, v, do = inputs(shape, seed=sum(shape), dtype=DTYPES[dt])
     log(f"fa_bwd without workspace {shape} {dt} {tiles}")
     got = _fa_bwd_no_workspace(q, k, v, do, tiles)
