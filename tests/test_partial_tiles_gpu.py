@@ -48,9 +48,9 @@ def test_forward_lse_any_length(dt, D):
     torch.cuda.synchronize()
     check_forward(o, q, k, v, label=f"partial fwd+lse {dt} D{D}")
     want = orc.lse_log2(q.double().cpu().numpy(), k.double().cpu().numpy())
-    # l sums P rounded to the element type: at most 2^-9 (bf16) / 2^-12 (fp16) relative,
-    # i.e. 2^-9 / ln 2 = 2.8e-3 in log2 units for bf16
-    tol = 3e-3 if dt == "bf16" else 1e-3
+    # l sums P rounded to the element type: at most 2^-8 (bf16) / 2^-11 (fp16) relative,
+    # i.e. 2^-8 / ln 2 = 5.6e-3 / 2^-11 / ln 2 = 7.0e-4 in log2 units
+    tol = 6e-3 if dt == "bf16" else 1e-3
     assert float(np.abs(lse.cpu().numpy() - want).max()) <= tol
 
 
