@@ -250,7 +250,7 @@ def kernel_flops_bytes(kernel, wl):
         return 2 * mm, e * S * D * (2 * B * H + 2 * B * Hkv)
     if kernel.startswith("dq_kernel"):
         return 3 * mm, e * S * D * (4 * B * H + 2 * B * Hkv) + 4 * B * H * S
-    if kernel.startswith("dkdv_kernel"):
+    if kernel.startswith("dkdv_kernel") or kernel.startswith("dkdv_pair_kernel"):
         return 4 * mm, e * S * D * (2 * B * H + 4 * B * Hkv) + 8 * B * H * S
     return 0.0, 4 * 2 * B * Hkv * S * D  # the split's reduction: fp32 partial sums read (per chunk, at least)
 
