@@ -36,9 +36,11 @@
 //     LDS arrays; the next tile's DMA runs while the current tile is computed.
 //   * V^T operands come from ds_read_b64_tr_b16 on the row-major V tile, so no
 //     transpose is ever materialised.
-//   * causal skipping at two levels: key tiles past the workgroup's last row are
-//     never loaded, and each wave skips 32-key blocks past its own last row;
-//     tiles wholly below the diagonal run a mask-free path.
+//   * causal skipping: key tiles past the workgroup's last row are never loaded;
+//     the tiles that meet the workgroup's diagonal run the full-tile schedule with
+//     the mask applied arithmetically, and a wave whose rows lie wholly before the
+//     last tile skips it.  The first reference point is S(0)'s row max, so no
+//     tile starts on the rescale path.
 //   * heavy-first, XCD-aware order: the 8 XCDs each take a contiguous range of
 //     (batch, head-group) units and dispatch the heaviest (last) query tiles of
 //     all their units first.
@@ -76,15 +78,10 @@ constexpr int fwd_waves_per_simd() {
   return (BN == 64 && (BM / 32) * GH >= 4) ? 2 : 1;
 }
 
-// Compile-time "tile is below the diagonal" marker, and its run-time twin.
+// Compile-time marker of a pipeline iteration that runs wholly below the diagonal.
 template <bool B>
 struct Tag {
   static constexpr bool value = B;
-  static constexpr bool is_dynamic = false;
-};
-struct Dyn {
-  bool value;
-  static constexpr bool is_dynamic = true;
 };
 
 // Two 8-byte transposed LDS reads -> one 16-byte MFMA operand.
@@ -228,47 +225,45 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
   float mrun = NEG_INF, lrun = 0.f;
 
-  // ---- pipeline stages.  `mt` is Tag<false> for tiles wholly below the
-  // diagonal (everything compile-time) or Dyn for the generic path, where
-  // `mt.value` says whether the tile straddles the diagonal (wave-uniform).
-  // Valid 32-key blocks of a tile for this wave (<= 0: none).
-  auto valid_blocks = [&](int k0, auto mt) __attribute__((always_inline)) {
-    if (!mt.value) return NB;
-    const int n = (q0 + 32 - k0) / 32;
-    return n > NB ? NB : n;
-  };
+  // ---- pipeline stages.  Every tile is computed whole (all NB 32-key blocks);
+  // on the tiles that meet the workgroup's diagonal the keys past each row are
+  // set to -inf arithmetically (mask_tile), so those tiles run the same
+  // branch-free schedule as the tiles below the diagonal, at the price of the
+  // MFMAs of blocks that lie wholly past a wave's rows.  With per-wave code for
+  // each block count the diagonal-region tiles took about twice a full tile.
 
   // S^T = K Q^T: A row c <- key 32nb + c; register g of lane (c, hh) holds
-  // key offset 8*(g/4) + 4*hh + (g%4) of the block, query c.  Keys past the
-  // query are set to -inf on the diagonal block.
-  auto s_tile = [&](const unsigned char* Ks, int k0, int nv, auto mt, f32x16 (&s)[NB]) __attribute__((always_inline)) {
+  // key offset 8*(g/4) + 4*hh + (g%4) of the block, query c.
+  auto s_tile = [&](const unsigned char* Ks, f32x16 (&s)[NB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      if (!mt.value || nb < nv) {
-        f32x16 x = f32x16{};
+      f32x16 x = f32x16{};
 #pragma unroll
-        for (int t = 0; t < KT; ++t) x = mfma32<E>(lds_read16(Ks, koff[t] + nb * 32 * ROWB), qf[t], x);
-        if (mt.value && k0 + 32 * nb == q0) {
-#pragma unroll
-          for (int g = 0; g < 16; ++g) {
-            const int koffs = 8 * (g >> 2) + 4 * hh + (g & 3);
-            if (koffs > c) x[g] = NEG_INF;
-          }
-        }
-        s[nb] = x;
-      }
+      for (int t = 0; t < KT; ++t) x = mfma32<E>(lds_read16(Ks, koff[t] + nb * 32 * ROWB), qf[t], x);
+      s[nb] = x;
     }
   };
 
-  // Row max of a tile in scaled log2 units (-inf where the wave has no valid block).
-  auto tile_max = [&](const f32x16 (&s)[NB], int nv, auto mt) __attribute__((always_inline)) {
+  // Causal mask of the tile starting at key k0: key k0 + 32nb + 8(g/4) + 4hh + (g%4)
+  // lies past row q0 + c exactly when 8(g/4) + (g%4) + (4hh - c) > q0 - k0 - 32nb.
+  const int lane_kq = 4 * hh - c;
+  auto mask_tile = [&](f32x16 (&s)[NB], int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int t = q0 - k0 - 32 * nb;
+#pragma unroll
+      for (int g = 0; g < 16; ++g)
+        if (lane_kq > t - (8 * (g >> 2) + (g & 3))) s[nb][g] = NEG_INF;
+    }
+  };
+
+  // Row max of a tile in scaled log2 units.
+  auto tile_max = [&](const f32x16 (&s)[NB]) __attribute__((always_inline)) {
     float mx = NEG_INF;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      if (!mt.value || nb < nv) {
 #pragma unroll
-        for (int g = 0; g < 16; ++g) mx = fmaxf(mx, s[nb][g]);
-      }
+      for (int g = 0; g < 16; ++g) mx = fmaxf(mx, s[nb][g]);
     return halfwave_max(mx) * scale_log2;
   };
 
@@ -287,60 +282,44 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
   // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7);
   // returns this lane's sum of the rounded P (v_dot2c with (1, 1)).
-  auto exp_tile = [&](const f32x16 (&s)[NB], int nv, auto mt, u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
+  auto exp_tile = [&](const f32x16 (&s)[NB], u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
     float lsum[2] = {0.f, 0.f};
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      if (!mt.value || nb < nv) {
-        float p[16];
+      float p[16];
 #pragma unroll
-        for (int g = 0; g < 16; ++g) p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
+      for (int g = 0; g < 16; ++g) p[g] = fast_exp2(__builtin_fmaf(s[nb][g], scale_log2, -mrun));
 #pragma unroll
-        for (int i1 = 0; i1 < 2; ++i1) {
-          u32x4 w;
+      for (int i1 = 0; i1 < 2; ++i1) {
+        u32x4 w;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
-            lsum[i1] = add_pair<E>(w[q], lsum[i1]);
-          }
-          pk[2 * nb + i1] = w;
+        for (int q = 0; q < 4; ++q) {
+          w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
+          lsum[i1] = add_pair<E>(w[q], lsum[i1]);
         }
+        pk[2 * nb + i1] = w;
       }
     }
     return lsum[0] + lsum[1];
   };
 
   // P of a tile against the lazy reference point, and the l update.  The
-  // first tile always takes the slow path (m = -inf gives p = inf).
-  auto softmax = [&](const f32x16 (&s)[NB], int nv, auto mt, u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
-    float ts = exp_tile(s, nv, mt, pk);
+  // reference point starts at the first tile's row max (taken after S(0)), so
+  // the first tile needs no rescale.
+  auto softmax = [&](const f32x16 (&s)[NB], u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
+    float ts = exp_tile(s, pk);
     if (__builtin_amdgcn_ballot_w64(!(ts <= kSumLimit))) {
-      rescale_to(tile_max(s, nv, mt));
-      ts = exp_tile(s, nv, mt, pk);
+      rescale_to(tile_max(s));
+      ts = exp_tile(s, pk);
     }
     lrun += ts;
   };
 
-  // O^T += V^T P^T; operand rows are d = 32db + pi(row), keys per slot as above.
-  auto pv = [&](const unsigned char* Vs, const u32x4 (&pk)[2 * NB], int nv, auto mt) __attribute__((always_inline)) {
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const int vb = ((db & 1) ? voff_odd : voff_even) + 64 * db;
-#pragma unroll
-      for (int u = 0; u < 2 * NB; ++u) {
-        if (!mt.value || (u >> 1) < nv) {
-          const int o = vb + 16 * u * ROWB;
-          acc[db] = mfma32<E>(lds_read_tr16x2(Vs, o, o + 8 * ROWB), pk[u], acc[db]);
-        }
-      }
-    }
-  };
-
-  // PV of a full tile with its V^T operands read two MFMAs ahead (three rotating
+  // O^T += V^T P^T with the V^T operands read two MFMAs ahead (three rotating
   // buffers, pinned by sched_barrier), the first two before the softmax, and the
-  // four d blocks' accumulators taking turns.  Left to itself the compiler read
-  // one operand ahead and waited on it before every MFMA.  Each accumulator sees
-  // the same MFMAs in the same order as in pv() (bitwise equal); 2 % faster.
+  // four d blocks' accumulators taking turns; operand rows are d = 32db + pi(row),
+  // keys per slot as above.  Left to itself the compiler read one operand ahead
+  // and waited on it before every MFMA (2 % slower).
   constexpr int NPV = DB * 2 * NB;
   u32x4 pvb[3];
   auto pv_read = [&](const unsigned char* Vs, int i) __attribute__((always_inline)) {
@@ -369,75 +348,65 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // V; both are double-buffered.  (The body is one scope with restrict-qualified
   // buffers: the tiles read are never the DMA targets, so the compiler need not
   // wait for the DMA before the transposed reads.)
+  // Iterations below the diagonal (ST) run only while tile j + 2 is below the
+  // workgroup's first row (j + 2 < jfull <= ntiles - 1, and j + 3 <= jfull for the
+  // second iteration of a pair): nothing is masked and the DMAs need no test
+  // (without the branches the DMA issue joins the tile's schedule: 2.3 % faster at
+  // B=4 H=32 S=4096 D=128).  The others (j + 1 < ntiles) mask S(j+1).
   auto body = [&](int j, const unsigned char* __restrict__ kcur, unsigned char* __restrict__ kdst,
                   const unsigned char* __restrict__ vcur, unsigned char* __restrict__ vdst,
-                  f32x16 (&sc)[NB], int nvc, f32x16 (&sn)[NB], int& nvn, auto mt) __attribute__((always_inline)) {
-    // Static (full-tile) iterations run only while tile j + 2 is below the workgroup's
-    // first row (j + 2 < jfull <= ntiles - 1, and j + 3 <= jfull for the second
-    // iteration of a pair), so their DMAs need no test: without the branches the
-    // DMA issue joins the tile's schedule (2.3 % faster at B=4 H=32 S=4096 D=128).
-    if constexpr (decltype(mt)::is_dynamic) {
-      if (j + 2 < ntiles) dma_k(j + 2, kdst);
-      if (j + 1 < ntiles) dma_v(j + 1, vdst);
-    } else {
+                  f32x16 (&sc)[NB], f32x16 (&sn)[NB], auto st) __attribute__((always_inline)) {
+    if constexpr (decltype(st)::value) {
       dma_k(j + 2, kdst);
-      dma_v(j + 1, vdst);
-    }
-    const Dyn cur{j >= jfull};
-    u32x4 pk[2 * NB];
-    if (!mt.value || j + 1 < ntiles) {
-      const Dyn nxt{j + 1 >= jfull};
-      nvn = mt.value ? valid_blocks((j + 1) * BN, nxt) : NB;
-      if constexpr (decltype(mt)::is_dynamic) {
-        s_tile(kcur, (j + 1) * BN, nvn, nxt, sn);
-        if (nvc == NB) {  // this wave's rows see every key of tile j: the full-tile PV
-          pv_pre(vcur);   // (1.4 % faster at B=4 H=32 S=4096 D=128 than pv() here)
-          softmax(sc, nvc, cur, pk);
-          pv_full(vcur, pk);
-        } else {
-          softmax(sc, nvc, cur, pk);
-          pv(vcur, pk, nvc, cur);
-        }
-      } else {
-        s_tile(kcur, (j + 1) * BN, NB, mt, sn);
-        pv_pre(vcur);
-        softmax(sc, NB, mt, pk);
-        pv_full(vcur, pk);
-      }
     } else {
-      softmax(sc, nvc, cur, pk);
-      pv(vcur, pk, nvc, cur);
+      if (j + 2 < ntiles) dma_k(j + 2, kdst);
     }
+    dma_v(j + 1, vdst);
+    u32x4 pk[2 * NB];
+    s_tile(kcur, sn);
+    if constexpr (!decltype(st)::value) mask_tile(sn, (j + 1) * BN);
+    pv_pre(vcur);
+    softmax(sc, pk);
+    pv_full(vcur, pk);
   };
-  auto iteration = [&](int j, f32x16 (&sc)[NB], int nvc, f32x16 (&sn)[NB], int& nvn, auto mt) __attribute__((always_inline)) {
+  auto iteration = [&](int j, f32x16 (&sc)[NB], f32x16 (&sn)[NB], auto st) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    body(j, Kbuf(j + 1), Kbuf(j), Vbuf(j), Vbuf(j + 1), sc, nvc, sn, nvn, mt);
+    body(j, Kbuf(j + 1), Kbuf(j), Vbuf(j), Vbuf(j + 1), sc, sn, st);
   };
 
-  // prologue: K(0), V(0), K(1) in flight; S(0)
+  // prologue: K(0), V(0), K(1) in flight; S(0) and its row max, the first reference
+  // point (key 0 lies at or below every row, so the max is finite)
   dma_k(0, Kbuf(0));
   dma_v(0, Vbuf(0));
   if (ntiles > 1) dma_k(1, Kbuf(1));
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   f32x16 sa[NB], sb[NB];
-  int nva, nvb = NB;
-  {
-    const Dyn m0{jfull == 0};
-    nva = valid_blocks(0, m0);
-    s_tile(Kbuf(0), 0, nva, m0, sa);
-  }
+  s_tile(Kbuf(0), sa);
+  if (jfull == 0) mask_tile(sa, 0);
+  mrun = tile_max(sa);
 
   // tiles j with j + 1 < jfull: both S(j) and S(j+1) below the diagonal
   int j = 0;
   for (; j + 2 < jfull; j += 2) {
-    iteration(j, sa, NB, sb, nvb, Tag<false>{});
-    iteration(j + 1, sb, NB, sa, nva, Tag<false>{});
+    iteration(j, sa, sb, Tag<true>{});
+    iteration(j + 1, sb, sa, Tag<true>{});
   }
-  for (; j < ntiles; j += 2) {
-    iteration(j, sa, nva, sb, nvb, Dyn{true});
-    if (j + 1 < ntiles) iteration(j + 1, sb, nvb, sa, nva, Dyn{true});
+  // the diagonal region (at most BM / BN + 2 tiles): S(j+1) masked, then moved into place
+  for (; j + 1 < ntiles; ++j) {
+    iteration(j, sa, sb, Tag<false>{});
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) sa[nb] = sb[nb];
+  }
+  // the last tile (no S to start); a wave whose rows lie wholly before it skips it
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (q0 + 31 >= j * BN) {
+    u32x4 pk[2 * NB];
+    pv_pre(Vbuf(j));
+    softmax(sa, pk);
+    pv_full(Vbuf(j), pk);
   }
 
   // ---- epilogue: O = acc / l; lane holds d = 32db + 16i1 + 8hh + 0..7
