@@ -1127,7 +1127,8 @@ void dq_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // work item: (b, h, query tile), XCD aware as the forward: XCD wg % 8 takes a
   // contiguous range of (b, h) and walks them in groups of xcd_group() heads, heaviest
   // query tiles of the group first (at B=4 H=32 S=4096 D=128, against all 16 heads of
-  // the XCD at once: one (b, h) after another -1.4 %, groups of 4 +1.5 %)
+  // the XCD at once: one (b, h) after another -1.4 %, groups of 4 +1.5 %, and about
+  // 1 % over groups of 8)
   const int nq = (S + BM - 1) / BM;
   const int nunits = B * H;
   const int wg = blockIdx.x;

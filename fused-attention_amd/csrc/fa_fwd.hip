@@ -125,8 +125,8 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   // their K/V) and walks them in groups of xcd_group() units, each group query tile
   // major with the heaviest tiles first, so the light tiles fill the end of every
   // group and of the kernel, and the units whose K/V the XCD streams at one time stay
-  // few.  At B=4 H=32 S=4096 D=128 (16 units per XCD), against all 16 units at once:
-  // one unit after another -2.7 %, groups of 2 / 4 / 8 units +2.1 / +3.3 / +4.0 %.
+  // few.  At B=4 H=32 S=4096 D=128 (16 units per XCD), against one unit after another:
+  // groups of 4 units about +6 %, groups of 8 about +4 %.
   const int nq = (S + BM - 1) / BM;  // the last query tile may be partial
   const int units_per_b = H / GH;
   const int nunits = B * units_per_b;
