@@ -853,7 +853,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int g = 8 * i1 + 2 * q;
-            bop[i1][q] = pack2<E>(to_f32<F16>(w[q] & 0xffffu) * x[qb][g], to_f32<F16>(w[q] >> 16) * x[qb][g + 1]);
+            bop[i1][q] = pack2<E>(mul_f16_f32<0>(w[q], x[qb][g]), mul_f16_f32<1>(w[q], x[qb][g + 1]));
           }
         }
       }
@@ -918,9 +918,14 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     const int qb = j >> 3, db = (j >> 1) & 3, i1 = j & 1;
     return tr_read2(buf + a2, to.tr(db, 2 * qb + i1, 0), to.tr(db, 2 * qb + i1, 1));
   };
-  // A stream also issues pair t+2's DMA, one part every other MFMA from the first,
-  // so the vector memory unit takes it in the background (issued together after
-  // the barrier, the eight waves' DMA stalled each of them by 300-500 cycles)
+  // A stream also issues pair t+2's DMA.  The source places one part every other
+  // MFMA from the first, but the parts' run-time tests (pair t+2 may not exist) are
+  // merged by the compiler into one block at the top of the stream, so the whole
+  // DMA goes out right after the barrier, its descriptors formed first.  Measured,
+  // that is the better place: with the parts pinned where the source puts them
+  // (the test made compile-time), the backward ran 2.0 % slower at B=4 H=32 S=4096
+  // D=128 and 8.1 % slower at GQA B=2 H=32 H_kv=8 S=4096: a part issued later has
+  // less of the stream to land in.
   auto stream0 = [&](int t, const u32x4 (&cur)[2][2], u32x4 (&nxt)[2][2]) __attribute__((always_inline)) {
     const bool dm = t + 2 < te;
     Dma job;
@@ -985,7 +990,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
       for (int q = q0; q < q0 + 2; ++q) {
         const int g = 8 * i1 + 2 * q;
         const uint32_t v = w[qb][i1][q];
-        bop[qb][i1][q] = pack2<E>(to_f32<F16>(v & 0xffffu) * x[qb][g], to_f32<F16>(v >> 16) * x[qb][g + 1]);
+        bop[qb][i1][q] = pack2<E>(mul_f16_f32<0>(v, x[qb][g]), mul_f16_f32<1>(v, x[qb][g + 1]));
       }
     };
     constexpr int PD = 3;

@@ -104,6 +104,21 @@ __device__ __forceinline__ float dot_pair<F16>(uint32_t a, uint32_t b, float acc
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
 }
 
+// The fp16 value in half `hi` of w, times x, in fp32 (v_fma_mix_f32 with a -0
+// addend: the widening is exact and the product rounds once, as in a widening
+// conversion followed by v_mul_f32, in one instruction instead of two).
+template <int HI>
+__device__ __forceinline__ float mul_f16_f32(uint32_t w, float x) {
+  // (the compiler folds fma(a, b, -0) into a multiply and keeps the widening apart)
+  float r;
+  const float nz = -0.0f;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(x), "v"(nz));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(x), "v"(nz));
+  return r;
+}
+
 // One 16-bit element -> fp32.
 template <typename E>
 __device__ __forceinline__ float to_f32(uint32_t bits16);
