@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fa {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -56,6 +58,30 @@ template <>
 __device__ __forceinline__ f32x16 mfma32<F16>(const u32x4& a, const u32x4& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x32_{bf16,f16}: C[16x16] += A[16x32] * B[32x16]; lane l holds
+// row / column l % 16 of A / B with k = 8 (l / 16) .. + 7, and C registers r of
+// lane l hold row 4 (l / 16) + r, column l % 16.
+template <typename E>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma16<BF16>(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma16<F16>(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
+}
+
+// Two 16-bit ones in one word.
+template <typename E>
+constexpr uint32_t ones2() {
+  return std::is_same<E, BF16>::value ? 0x3F803F80u : 0x3C003C00u;
 }
 
 // Two fp32 -> one 32-bit word holding two 16-bit values (x in the low half).

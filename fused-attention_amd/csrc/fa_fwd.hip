@@ -16,7 +16,7 @@
 // reference's tolerance: l sums the rounded P that the PV product uses (the
 // reference sums the unrounded p, fused.py:59), so O is an exactly normalised
 // average of the V rows it weights; and the reference point m is lazy: a tile's
-// p is computed against the current m, and only if some lane's sum of p over
+// p is computed against the current m, and only if some row's sum of p over
 // the tile exceeds 2^FA_RESCALE_THRESHOLD (or is not finite) is the tile's row
 // max taken, acc and l rescaled and p recomputed.  Every p therefore stays
 // <= 2^T, no row max is reduced on the common path, and O = acc / l and
@@ -66,7 +66,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 constexpr int kWaitVmcnt0 = 0x0F70;
-// p is recomputed against a fresh row max only when a lane's sum of p over a
+// p is recomputed against a fresh row max only when a row's sum of p over a
 // tile exceeds 2^FA_RESCALE_THRESHOLD
 #ifndef FA_RESCALE_THRESHOLD
 #define FA_RESCALE_THRESHOLD 8
@@ -223,7 +223,18 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
-  float mrun = NEG_INF, lrun = 0.f;
+  float mrun = NEG_INF;
+  // Row sums of P on the matrix pipe.  Fed as the B operand of a 16x16x32 MFMA, a
+  // k-step u of P^T puts query n's 16 keys (both half-waves) in the k groups 0 and
+  // 2 of column n and query n + 16's in groups 1 and 3 (n = lane % 16); against the
+  // 0/1 selector rsel (ones in lanes 0 and 32, row 0, and 17 and 49, row 1) the
+  // product's row 0 / row 1 hold those two queries' sums: lane n, registers 0 and 1.
+  // lsum keeps l in that layout.  One such MFMA per k-step replaces eight
+  // v_dot2c_f32_*, each of which stalls the matrix pipe of its SIMD for about 16
+  // cycles on gfx950 (an issue-rate probe), where the MFMA takes its 16.
+  const uint32_t one = (lane == 0 || lane == 32 || lane == 17 || lane == 49) ? ones2<E>() : 0u;
+  const u32x4 rsel = {one, one, one, one};
+  f32x4 lsum = f32x4{};
 
   // ---- pipeline stages.  Every tile is computed whole (all NB 32-key blocks);
   // on the tiles that meet the workgroup's diagonal the keys past each row are
@@ -272,7 +283,8 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const float mnew = fmaxf(mrun, mx);
     const float alpha = fast_exp2(mrun - mnew);
     mrun = mnew;
-    lrun *= alpha;
+    lsum[0] *= alpha;                    // query lane % 16: this lane's own alpha
+    lsum[1] *= __shfl_xor(alpha, 16);    // query lane % 16 + 16
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -281,9 +293,9 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 
   // P^T as the B operand of the PV MFMAs: k-step u = 2nb + i1 holds
   // keys 32nb + 16i1 + 4hh + {0..3} (slots 0-3) and +8 (slots 4-7);
-  // returns this lane's sum of the rounded P (v_dot2c with (1, 1)).
+  // returns the tile's sums of the rounded P in lsum's layout.
   auto exp_tile = [&](const f32x16 (&s)[NB], u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
-    float lsum[2] = {0.f, 0.f};
+    f32x4 ts = f32x4{};
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       float p[16];
@@ -295,24 +307,25 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           w[q] = pack2<E>(p[8 * i1 + 2 * q], p[8 * i1 + 2 * q + 1]);
-          lsum[i1] = add_pair<E>(w[q], lsum[i1]);
         }
         pk[2 * nb + i1] = w;
+        ts = mfma16<E>(rsel, w, ts);
       }
     }
-    return lsum[0] + lsum[1];
+    return ts;
   };
 
   // P of a tile against the lazy reference point, and the l update.  The
   // reference point starts at the first tile's row max (taken after S(0)), so
   // the first tile needs no rescale.
   auto softmax = [&](const f32x16 (&s)[NB], u32x4 (&pk)[2 * NB]) __attribute__((always_inline)) {
-    float ts = exp_tile(s, pk);
-    if (__builtin_amdgcn_ballot_w64(!(ts <= kSumLimit))) {
+    f32x4 ts = exp_tile(s, pk);
+    if (__builtin_amdgcn_ballot_w64(!(ts[0] <= kSumLimit && ts[1] <= kSumLimit))) {
       rescale_to(tile_max(s));
       ts = exp_tile(s, pk);
     }
-    lrun += ts;
+    lsum[0] += ts[0];
+    lsum[1] += ts[1];
   };
 
   // O^T += V^T P^T with the V^T operands read two MFMAs ahead (three rotating
@@ -410,7 +423,9 @@ void fwd_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   }
 
   // ---- epilogue: O = acc / l; lane holds d = 32db + 16i1 + 8hh + 0..7
-  const float ltot = halfwave_sum(lrun);
+  // l of query c from lane c % 16 (register 0 for c < 16, 1 above)
+  const float l_lo = __shfl(lsum[0], c & 15), l_hi = __shfl(lsum[1], c & 15);
+  const float ltot = c < 16 ? l_lo : l_hi;
   const float inv = 1.0f / ltot;
   uint16_t* orow = O + qbase + (size_t)m * D;
   if (m < S) {  // rows of a partial last query tile past S are not stored
