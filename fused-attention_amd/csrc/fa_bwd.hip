@@ -682,35 +682,79 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   const int role = wave / NKB, kb = wave % NKB;
   const int c = lane & 31, hh = lane >> 5;
 
-  // work item: as in dkdv_kernel
+  // ---- work items: key tile jt of chunk hc of K/V head bkv (u = bkv nsplit + hc),
+  // L = u nk + jt, the items of XCD x either the range [x total/8, (x+1) total/8) or
+  // (total not a multiple of 8) L = 8i + x; within a head the heaviest key tiles
+  // come first.  The grid holds only the workgroups that run at once (one per CU):
+  // slot wg / 8 of XCD wg % 8 takes its XCD's items in rounds of gridDim.x / 8 items,
+  // mirrored in odd rounds, so a heavy key tile and a light one pair up.  While an
+  // item's last two pairs run, the next item's first two pairs and its K/V rows are
+  // loaded (a workgroup's start-up, ~6 us of a ~57 us item at B=4 H=32 S=4096 D=128,
+  // otherwise leaves its CU idle).
   const int G = H / Hkv;
   const int nk = (S + BNK - 1) / BNK;
   const int total = B * Hkv * nsplit * nk;
+  const int nq = (S + BMQ - 1) / BMQ;
   const int wg = blockIdx.x;
-  const int L = (total % 8 == 0) ? (wg % 8) * (total / 8) + (wg / 8) : wg;
-  const int u = L / nk, jt = L % nk;
-  const int bkv = u / nsplit;
-  const size_t base = (size_t)bkv * S * D;
-  const int bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;
+  const int slots = (int)gridDim.x / 8, my_slot = wg / 8, xcd = wg % 8;
+  auto item_L = [&](int k) __attribute__((always_inline)) {  // -1: no k-th item
+    const int i = k * slots + ((k & 1) ? slots - 1 - my_slot : my_slot);
+    if (total % 8 == 0) return i < total / 8 ? xcd * (total / 8) + i : -1;
+    const int L = 8 * i + xcd;
+    return L < total ? L : -1;
+  };
+  struct KItem {
+    int u, jt, bh0, i0, tb, te;
+    size_t base;
+  };
+  auto make_item = [&](int L) __attribute__((always_inline)) {
+    KItem it;
+    it.u = L / nk;
+    it.jt = L % nk;
+    const int bkv = it.u / nsplit;
+    it.base = (size_t)bkv * S * D;
+    it.bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;
+    it.i0 = (it.jt * BNK) / BMQ;
+    const int T = G * (nq - it.i0), hc = it.u % nsplit;
+    it.tb = (int)((long long)T * hc / nsplit);
+    it.te = (int)((long long)T * (hc + 1) / nsplit);
+    return it;
+  };
+  const int L0 = item_L(0);
+  if (L0 < 0) return;  // the grid is rounded up to a multiple of 8
 
-  const int k0w = jt * BNK + 32 * kb;     // first key of this wave's block
-  const int n = k0w + c;                  // this lane's key
-  const bool active = k0w < S;            // wave-uniform
+  // the current item, as the code below reads it, and the next one (plain scalars:
+  // as structs chosen at run time they went to scratch memory)
+  int u, jt, bh0, i0, tb, te, k0w, n;
+  size_t base;
+  bool active;
+  int n_u = 0, n_jt = 0, n_bh0 = 0, n_i0 = 0, n_tb = 0, n_te = 0;
+  size_t n_base = 0;
+  bool has_next = false;
+  auto set_item = [&](const KItem& it) __attribute__((always_inline)) {
+    u = it.u;
+    jt = it.jt;
+    bh0 = it.bh0;
+    i0 = it.i0;
+    tb = it.tb;
+    te = it.te;
+    base = it.base;
+    k0w = jt * BNK + 32 * kb;   // first key of this wave's block
+    n = k0w + c;                // this lane's key
+    active = k0w < S;           // wave-uniform
+  };
+  set_item(make_item(L0));
 
   // K (role 0) or V (role 1) rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
   u32x4 xf[KT];
-  if (active) {
-    const uint16_t* xr = (role ? V : K) + base + (size_t)min(n, S - 1) * D + 8 * hh;
+  auto load_xf = [&](int xjt, size_t xbase) __attribute__((always_inline)) {
+    const int kw = xjt * BNK + 32 * kb;
+    if (kw < S) {
+      const uint16_t* xr = (role ? V : K) + xbase + (size_t)min(kw + c, S - 1) * D + 8 * hh;
 #pragma unroll
-    for (int t = 0; t < KT; ++t) xf[t] = gload16(xr + 16 * t);
-  }
-
-  const int nq = (S + BMQ - 1) / BMQ;
-  const int i0 = (jt * BNK) / BMQ;
-  const int NI = nq - i0;
-  const int T = G * NI;
-  const int hc = u % nsplit;
-  const int tb = (int)((long long)T * hc / nsplit), te = (int)((long long)T * (hc + 1) / nsplit);
+      for (int t = 0; t < KT; ++t) xf[t] = gload16(xr + 16 * t);
+    }
+  };
 
   // DMA of pair (di, dg)'s Q and dO tiles and its two row-term slices: every wave
   // copies NDMA 1 KB blocks of each tile, waves 0 and 1 one slice each
@@ -721,27 +765,41 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     const int row = (wave + x * NW) * (1024 / ROWB) + drow;
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
+  // pair p of the current item sits in buffer (p + boff) % NBUF; boff carries the
+  // rotation into the next item (whose first pairs are loaded during this one)
+  int boff = 0;
   auto bufp = [&](int t) __attribute__((always_inline)) {
-    return bufs + __builtin_amdgcn_readfirstlane((t % NBUF) * BUFA);
+    return bufs + __builtin_amdgcn_readfirstlane(((t + boff) % NBUF) * BUFA);
   };
-  int di = i0 + tb / G, dg = tb % G;
-  // the next pair's descriptors (advancing the sequence), and its DMA in
+  // pair p of item it: query tile i0 + p / G of query head bh0 + p % G; its DMA in
   // 2 NDMA + 1 parts: part 2x / 2x+1 = block x of the Q / dO tile, part 2 NDMA =
   // the row-term slice (waves 0 and 1)
   struct Dma {
     __amdgpu_buffer_rsrc_t q, d, r;
     unsigned char* buf;
   };
-  auto dma_prep = [&](unsigned char* buf) __attribute__((always_inline)) {
+  auto dma_prep = [&](int bh0, int qi0, int p, unsigned char* buf) __attribute__((always_inline)) {
+    const int di = qi0 + p / G, dg = p % G;
     const size_t row0 = (size_t)(bh0 + dg) * S + (size_t)di * BMQ;
     const int rows = min(BMQ, S - di * BMQ);
     Dma j{make_rsrc(Q + row0 * D, rows * ROWB), make_rsrc(dO + row0 * D, rows * ROWB),
           make_rsrc(Rb + (wave == 1 ? (size_t)B * H * S : 0) + row0, rows * 4), buf};
-    if (++dg == G) {
-      dg = 0;
-      ++di;
-    }
     return j;
+  };
+  // the pair at position p of the current item's sequence, continued into the next
+  // item's first two pairs (false: none)
+  auto dma_at = [&](int p, int& dbh0, int& qi0, int& pp) __attribute__((always_inline)) {
+    if (p < te) {
+      dbh0 = bh0;
+      qi0 = i0;
+      pp = p;
+      return true;
+    }
+    if (!has_next) return false;
+    dbh0 = n_bh0;
+    qi0 = n_i0;
+    pp = n_tb + (p - te);
+    return pp < n_te;
   };
   auto dma_part = [&](const Dma& j, int k) __attribute__((always_inline)) {
     if (k < 2 * NDMA) {
@@ -751,8 +809,8 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
       dma4(j.r, j.buf + OFF_L + wave * 4 * BMQ, 4 * lane, 0);
     }
   };
-  auto dma_next = [&](unsigned char* buf) __attribute__((always_inline)) {
-    const Dma j = dma_prep(buf);
+  auto dma_pair = [&](int bh0, int qi0, int p, unsigned char* buf) __attribute__((always_inline)) {
+    const Dma j = dma_prep(bh0, qi0, p, buf);
 #pragma unroll
     for (int k = 0; k <= 2 * NDMA; ++k) dma_part(j, k);
   };
@@ -871,7 +929,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   // the rest lie wholly past them.  Only the last key tile can have inactive waves,
   // and it meets at most two query tiles (NI <= 2), so the full paths need no
   // activity test.
-  const int TE = G * min(2, NI);
+  int TE = G * min(2, nq - i0);
   // pair t+1 has landed, P(t) is visible, and nobody reads pair t-1's buffer or
   // slot (t+1) % 2 any more
   auto sync = [&]() __attribute__((always_inline)) {
@@ -880,15 +938,54 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   };
   auto top = [&](int t) __attribute__((always_inline)) {
     sync();
-    if (t + 2 < te) dma_next(bufp(t + 2));
+    int dbh, dqi, dpp;
+    if (dma_at(t + 2, dbh, dqi, dpp)) dma_pair(dbh, dqi, dpp, bufp(t + 2));
+    // the item's last pair: its K/V rows are used no more, the next item's load
+    if (t == te - 1 && has_next) load_xf(n_jt, n_base);
   };
   f32x16 x[2];
   u32x4 pk[2][2], pkn[2][2];
-  if (tb < te) {  // (a chunk of a light key tile can be empty: it stores zeros)
-    dma_next(bufp(tb));
-    if (tb + 1 < te) dma_next(bufp(tb + 1));
-    // pair tb has landed once at most pair tb+1's operations are outstanding
-    if (tb + 1 < te) {
+  // the item's first pairs (those not loaded during the previous item), then S / dP
+  // of its first pair
+  int pre = 0;        // bit i: pair tb + i of this item already in flight
+  bool xf_pre = false;
+  bool first = true;
+  // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7; role 0 stores
+  // dV, role 1 dK (keys past S: nothing)
+  auto epilogue = [&]() __attribute__((always_inline)) {
+    if (!active || n >= S) return;
+    const float mul = role ? sm_scale : 1.0f;
+    if (nsplit > 1) {  // fp32 partial sums of this chunk, dK already scaled
+      float* pr = (role ? Pk : Pv) + ((size_t)u * S + n) * D;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) {
+          const int d0 = db * 32 + 16 * i1 + 8 * hh;
+#pragma unroll
+          for (int h4 = 0; h4 < 2; ++h4) {
+            const int g0 = 8 * i1 + 4 * h4;
+            gstore_f32x4(pr + d0 + 4 * h4, f32x4{acc[db][g0] * mul, acc[db][g0 + 1] * mul,
+                                                 acc[db][g0 + 2] * mul, acc[db][g0 + 3] * mul});
+          }
+        }
+      return;
+    }
+    uint16_t* r = (role ? dK : dV) + base + (size_t)n * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i1 = 0; i1 < 2; ++i1) gstore16(r + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, mul));
+  };
+  auto prologue = [&]() __attribute__((always_inline)) {
+    if (!xf_pre) load_xf(jt, base);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
+    if (tb >= te) return;  // (a chunk of a light key tile can be empty: it stores zeros)
+    if (!(pre & 1)) dma_pair(bh0, i0, tb, bufp(tb));
+    if (tb + 1 < te && !(pre & 2)) dma_pair(bh0, i0, tb + 1, bufp(tb + 1));
+    if (first && tb + 1 < te) {
+      // pair tb has landed once at most pair tb+1's operations are outstanding
       if (wave < 2) __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA + 1));
       else __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA));
     } else {
@@ -897,7 +994,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     __syncthreads();
     if (tb >= TE) front(tb, x, pk, BTag<true>{});
     else front(tb, x, pk, BTag<false>{});
-  }
+  };
   // Full pairs with a next pair run as one stream of 32 MFMAs per wave, operand
   // reads issued three MFMAs ahead (a rotating set of four, pinned by
   // sched_barrier; left to itself the compiler issued each read just before its
@@ -926,10 +1023,11 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   // (the test made compile-time), the backward ran 2.0 % slower at B=4 H=32 S=4096
   // D=128 and 8.1 % slower at GQA B=2 H=32 H_kv=8 S=4096: a part issued later has
   // less of the stream to land in.
-  auto stream0 = [&](int t, const u32x4 (&cur)[2][2], u32x4 (&nxt)[2][2]) __attribute__((always_inline)) {
-    const bool dm = t + 2 < te;
+  auto stream0 = [&](int t, const u32x4 (&pcur)[2][2], u32x4 (&pnxt)[2][2]) __attribute__((always_inline)) {
+    int dbh, dqi, dpp;
+    const bool dm = dma_at(t + 2, dbh, dqi, dpp);
     Dma job;
-    if (dm) job = dma_prep(bufp(t + 2));
+    if (dm) job = dma_prep(dbh, dqi, dpp, bufp(t + 2));
     const unsigned char* bn = bufp(t + 1);
     const unsigned char* bc = bufp(t);
     x[0] = load_rows(reinterpret_cast<const float*>(bn + lo), 0);
@@ -942,13 +1040,13 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
 #pragma unroll
       for (int e = 0; e < 4; ++e) p[e] = fast_exp2(x[qb][4 * k + e] * scale_log2);
       const int i1 = k >> 1, q0 = 2 * (k & 1);
-      nxt[qb][i1][q0] = pack2<E>(p[0], p[1]);
-      nxt[qb][i1][q0 + 1] = pack2<E>(p[2], p[3]);
+      pnxt[qb][i1][q0] = pack2<E>(p[0], p[1]);
+      pnxt[qb][i1][q0 + 1] = pack2<E>(p[2], p[3]);
       if constexpr (!PF16) {
         hp[qb][i1][q0] = pack2<F16>(p[0], p[1]);
         hp[qb][i1][q0 + 1] = pack2<F16>(p[2], p[3]);
       }
-      if (k & 1) *slot(t + 1, qb, i1) = PF16 ? nxt[qb][i1] : hp[qb][i1];
+      if (k & 1) *slot(t + 1, qb, i1) = PF16 ? pnxt[qb][i1] : hp[qb][i1];
     };
     constexpr int PD = 3;
     u32x4 rot[PD + 1];
@@ -963,7 +1061,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
         x[i & 1] = mfma32<E>(rot[i % (PD + 1)], xf[i >> 1], x[i & 1]);
       } else {
         constexpr int j = i - 16, qb = j >> 3, db = (j >> 1) & 3, i1 = j & 1;
-        acc[db] = mfma32<E>(rot[i % (PD + 1)], cur[qb][i1], acc[db]);
+        acc[db] = mfma32<E>(rot[i % (PD + 1)], pcur[qb][i1], acc[db]);
       }
       // S of block 0 is complete after MFMA 14, of block 1 after 15
       if constexpr (i >= 17 && i <= 23 && (i - 17) % 2 == 0) p_chunk(0, (i - 17) / 2);
@@ -972,9 +1070,10 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     });
   };
   auto stream1 = [&](int t) __attribute__((always_inline)) {
-    const bool dm = t + 2 < te;
+    int dbh, dqi, dpp;
+    const bool dm = dma_at(t + 2, dbh, dqi, dpp);
     Dma job;
-    if (dm) job = dma_prep(bufp(t + 2));
+    if (dm) job = dma_prep(dbh, dqi, dpp, bufp(t + 2));
     const unsigned char* bn = bufp(t + 1);
     const unsigned char* bc = bufp(t);
     u32x4 w[2][2], bop[2][2];
@@ -1021,78 +1120,93 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     });
   };
 
-  // The two roles run separate loops with the same barriers, so each keeps only its
-  // own state in registers.  Role 0 alternates the two packed-P register sets by
-  // unrolling two pairs.
-  int t = tb;
+  // per item: the next item's descriptor, the edge-pair count, the prologue
+  auto begin_item = [&](int k) __attribute__((always_inline)) {
+    const int Ln = item_L(k + 1);
+    has_next = Ln >= 0;
+    if (has_next) {
+      const KItem it = make_item(Ln);
+      n_u = it.u;
+      n_jt = it.jt;
+      n_bh0 = it.bh0;
+      n_i0 = it.i0;
+      n_tb = it.tb;
+      n_te = it.te;
+      n_base = it.base;
+    }
+    TE = G * min(2, nq - i0);
+    prologue();
+  };
+  // to the next item: its first pair at position te is in flight if iteration te - 2
+  // ran, its second at te + 1 if iteration te - 1 ran (which also loaded its K/V rows)
+  auto next_item = [&]() __attribute__((always_inline)) {
+    const int nn = n_te - n_tb;
+    pre = ((te - tb >= 2 && nn >= 1) ? 1 : 0) | ((te - tb >= 1 && nn >= 2) ? 2 : 0);
+    xf_pre = te - tb >= 1;
+    boff = ((boff + te - n_tb) % NBUF + NBUF) % NBUF;
+    first = false;
+    set_item(KItem{n_u, n_jt, n_bh0, n_i0, n_tb, n_te, n_base});
+  };
+
+  // The two roles run separate loops with the same barriers per item, so each keeps
+  // only its own state in registers.  Role 0 alternates the two packed-P register
+  // sets by unrolling two pairs.
   if (role == 0) {
-    auto step = [&](int t, u32x4 (&cur)[2][2], u32x4 (&nxt)[2][2], auto full) __attribute__((always_inline)) {
+    auto step = [&](int t, u32x4 (&pc)[2][2], u32x4 (&pn)[2][2], auto full) __attribute__((always_inline)) {
       top(t);
-      if (t + 1 < te) front(t + 1, x, nxt, full);
-      back(t, x, cur, full);
+      if (t + 1 < te) front(t + 1, x, pn, full);
+      back(t, x, pc, full);
     };
-    for (; t < min(te, TE); ++t) {  // edge pairs: at most two per K/V head
-      step(t, pk, pkn, BTag<false>{});
+    for (int k = 0;; ++k) {
+      begin_item(k);
+      int t = tb;
+      for (; t < min(te, TE); ++t) {  // edge pairs: at most two per K/V head
+        step(t, pk, pkn, BTag<false>{});
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
-    }
-    for (; t + 2 < te; t += 2) {
-      sync();
-      stream0(t, pk, pkn);
-      sync();
-      stream0(t + 1, pkn, pk);
-    }
-    for (; t < te; ++t) {
-      step(t, pk, pkn, BTag<true>{});
+          for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
+      }
+      for (; t + 2 < te; t += 2) {
+        sync();
+        stream0(t, pk, pkn);
+        sync();
+        stream0(t + 1, pkn, pk);
+      }
+      for (; t < te; ++t) {
+        step(t, pk, pkn, BTag<true>{});
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
+          for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
+      }
+      epilogue();
+      if (!has_next) break;
+      next_item();
     }
   } else {
-    for (; t < min(te, TE); ++t) {
-      top(t);
-      back(t, x, pk, BTag<false>{});
-      if (t + 1 < te) front(t + 1, x, pkn, BTag<false>{});
-    }
-    for (; t + 1 < te; ++t) {
-      sync();
-      stream1(t);
-    }
-    for (; t < te; ++t) {
-      top(t);
-      back(t, x, pk, BTag<true>{});
-      if (t + 1 < te) front(t + 1, x, pkn, BTag<true>{});
-    }
-  }
-
-  // ---- epilogue: lane holds key n, d = 32db + 16i1 + 8hh + 0..7; role 0 stores
-  // dV, role 1 dK
-  if (!active || n >= S) return;
-  const float mul = role ? sm_scale : 1.0f;
-  if (nsplit > 1) {  // fp32 partial sums of this chunk, dK already scaled
-    float* pr = (role ? Pk : Pv) + ((size_t)u * S + n) * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i1 = 0; i1 < 2; ++i1) {
-        const int d0 = db * 32 + 16 * i1 + 8 * hh;
-#pragma unroll
-        for (int h4 = 0; h4 < 2; ++h4) {
-          const int g0 = 8 * i1 + 4 * h4;
-          gstore_f32x4(pr + d0 + 4 * h4, f32x4{acc[db][g0] * mul, acc[db][g0 + 1] * mul,
-                                               acc[db][g0 + 2] * mul, acc[db][g0 + 3] * mul});
-        }
+    for (int k = 0;; ++k) {
+      begin_item(k);
+      int t = tb;
+      for (; t < min(te, TE); ++t) {
+        top(t);
+        back(t, x, pk, BTag<false>{});
+        if (t + 1 < te) front(t + 1, x, pkn, BTag<false>{});
       }
-    return;
+      for (; t + 1 < te; ++t) {
+        sync();
+        stream1(t);
+      }
+      for (; t < te; ++t) {
+        top(t);
+        back(t, x, pk, BTag<true>{});
+        if (t + 1 < te) front(t + 1, x, pkn, BTag<true>{});
+      }
+      epilogue();
+      if (!has_next) break;
+      next_item();
+    }
   }
-  uint16_t* r = (role ? dK : dV) + base + (size_t)n * D;
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int i1 = 0; i1 < 2; ++i1) gstore16(r + db * 32 + 16 * i1 + 8 * hh, pack8<E>(acc[db], 8 * i1, mul));
 }
 
 // ===========================================================================
@@ -1451,7 +1565,10 @@ static bool launch_dkdv(const BwdArgs& a) {
   bool paired = false;
   if constexpr (FA_DKDV_PAIR && D == 128) {
     if (a.rowb) {
-      hipLaunchKernelGGL((dkdv_pair_kernel<E, D, BMQ, BNK>), grid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
+      // one workgroup per CU walks the key tiles (the kernel reads the grid size)
+      const auto kern = dkdv_pair_kernel<E, D, BMQ, BNK>;
+      const dim3 pgrid(resident_grid((int)grid.x, (const void*)kern, 4 * BNK));
+      hipLaunchKernelGGL(kern, pgrid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
                          (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.d_o,
                          a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,
                          nsplit, a.B, a.H, a.Hkv, a.S, a.scale_log2, a.sm_scale);

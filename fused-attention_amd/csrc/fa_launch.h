@@ -57,6 +57,23 @@ inline bool smem_attr(const void* kern) {
   return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, SMEM) == hipSuccess;
 }
 
+// Grid of a kernel whose workgroups walk their share of `items` work items: the item
+// count rounded up to a multiple of 8 (workgroups reach the 8 XCDs in turn), capped
+// at the workgroups the device runs at once (its CUs times the kernel's occupancy,
+// rounded down to a multiple of 8).
+inline int resident_grid(int items, const void* kern, int threads) {
+  const int all = (items + 7) / 8 * 8;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return all;
+  }
+  const int resident = cus * per_cu / 8 * 8;
+  return resident >= 8 && resident < all ? resident : all;
+}
+
 #define set_smem_once(kern, SMEM)                                   \
   ([&]() {                                                          \
     static const bool ok_ = ::fa::smem_attr<SMEM>(kern);            \
