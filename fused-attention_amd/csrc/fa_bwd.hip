@@ -1567,7 +1567,8 @@ static bool launch_dkdv(const BwdArgs& a) {
     if (a.rowb) {
       // one workgroup per CU walks the key tiles (the kernel reads the grid size)
       const auto kern = dkdv_pair_kernel<E, D, BMQ, BNK>;
-      const dim3 pgrid(resident_grid((int)grid.x, (const void*)kern, 4 * BNK));
+      static const int per_cu = occupancy_per_cu((const void*)kern, 4 * BNK);  // (thread-safe init)
+      const dim3 pgrid(resident_grid((int)grid.x, per_cu));
       hipLaunchKernelGGL(kern, pgrid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
                          (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.d_o,
                          a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,

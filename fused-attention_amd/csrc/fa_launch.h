@@ -59,19 +59,29 @@ inline bool smem_attr(const void* kern) {
 
 // Grid of a kernel whose workgroups walk their share of `items` work items: the item
 // count rounded up to a multiple of 8 (workgroups reach the 8 XCDs in turn), capped
-// at the workgroups the device runs at once (its CUs times the kernel's occupancy,
-// rounded down to a multiple of 8).
-inline int resident_grid(int items, const void* kern, int threads) {
+// at the workgroups the device runs at once (its CUs times the kernel's occupancy
+// per_cu, rounded down to a multiple of 8).
+inline int resident_grid(int items, int per_cu) {
   const int all = (items + 7) / 8 * 8;
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess) {
+  int dev = 0, cus = 0;
+  if (per_cu <= 0 || hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
     (void)hipGetLastError();
     return all;
   }
   const int resident = cus * per_cu / 8 * 8;
   return resident >= 8 && resident < all ? resident : all;
+}
+
+// Workgroups of `kern` (launched with `threads` threads) that one CU holds at once;
+// 0 if the runtime cannot tell.
+inline int occupancy_per_cu(const void* kern, int threads) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return per_cu;
 }
 
 #define set_smem_once(kern, SMEM)                                   \
