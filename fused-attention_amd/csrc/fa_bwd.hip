@@ -645,7 +645,9 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 // registers); role 1 adds pair t to dK (P(t) from LDS, dP(t) kept from the
 // previous iteration), then forms dP of pair t+1.  Each SIMD thus mixes the
 // full-rate operand reads of one product with the transposed reads of the
-// other throughout the iteration.  P of pair t sits in slot t % 2.
+// other throughout the iteration.  P of pair t sits in slot t % 2.  The grid holds
+// one workgroup per CU, each walking a fixed share of the key tiles (see the work
+// items below) with the next tile's first pairs loaded under the current one's last.
 template <typename E, int D, int BMQ, int BNK>
 __global__ __launch_bounds__(4 * BNK)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
