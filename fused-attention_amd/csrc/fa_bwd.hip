@@ -648,7 +648,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 // other throughout the iteration.  P of pair t sits in slot t % 2.  The grid holds
 // one workgroup per CU, each walking a fixed share of the key tiles (see the work
 // items below) with the next tile's first pairs loaded under the current one's last.
-template <typename E, int D, int BMQ, int BNK>
+template <typename E, int D, int BMQ, int BNK, bool WALK>
 __global__ __launch_bounds__(4 * BNK)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -693,6 +693,17 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   // item's last two pairs run, the next item's first two pairs and its K/V rows are
   // loaded (a workgroup's start-up, ~6 us of a ~57 us item at B=4 H=32 S=4096 D=128,
   // otherwise leaves its CU idle).
+  // An item's pairs: the key tile's walk index w = G (di - i0) + dg covers query tiles
+  // di >= i0 (its diagonal tile) of the G query heads bh0 + dg.  Without WALK, chunk hc
+  // is the range [T hc / nsplit, T (hc+1) / nsplit) of the T = G (nq - i0) indices,
+  // run upward from the diagonal.  With WALK (chosen when a K/V head's G heads of Q
+  // and dO exceed the L2), chunk hc takes the w with w % nsplit == hc, and items of
+  // even rounds run their chunk from the last query tile down, odd rounds from the
+  // diagonal up: the slots of an XCD all start an even round at the last query tile,
+  // and each starts its odd-round item (diagonal two tiles below where its even-round
+  // item ended) at the time the others pass that tile, so the XCD's workgroups read
+  // the same Q/dO tiles at about the same time and each is fetched about once, not
+  // once per key tile.
   const int G = H / Hkv;
   const int nk = (S + BNK - 1) / BNK;
   const int total = B * Hkv * nsplit * nk;
@@ -706,10 +717,10 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     return L < total ? L : -1;
   };
   struct KItem {
-    int u, jt, bh0, i0, tb, te;
+    int u, jt, bh0, i0, hc, rev, tb, te;
     size_t base;
   };
-  auto make_item = [&](int L) __attribute__((always_inline)) {
+  auto make_item = [&](int L, int k) __attribute__((always_inline)) {
     KItem it;
     it.u = L / nk;
     it.jt = L % nk;
@@ -718,8 +729,16 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     it.bh0 = (bkv / Hkv) * H + (bkv % Hkv) * G;
     it.i0 = (it.jt * BNK) / BMQ;
     const int T = G * (nq - it.i0), hc = it.u % nsplit;
-    it.tb = (int)((long long)T * hc / nsplit);
-    it.te = (int)((long long)T * (hc + 1) / nsplit);
+    it.hc = hc;
+    if constexpr (WALK) {
+      it.rev = (k & 1) ? 0 : 1;
+      it.tb = 0;
+      it.te = T > hc ? (T - hc + nsplit - 1) / nsplit : 0;
+    } else {
+      it.rev = 0;
+      it.tb = (int)((long long)T * hc / nsplit);
+      it.te = (int)((long long)T * (hc + 1) / nsplit);
+    }
     return it;
   };
   const int L0 = item_L(0);
@@ -727,10 +746,11 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
 
   // the current item, as the code below reads it, and the next one (plain scalars:
   // as structs chosen at run time they went to scratch memory)
-  int u, jt, bh0, i0, tb, te, k0w, n;
+  // an item's sequence runs over positions tb .. te-1 (tb = 0 with WALK)
+  int u, jt, bh0, i0, hc, rev, tb, te, k0w, n;
   size_t base;
   bool active;
-  int n_u = 0, n_jt = 0, n_bh0 = 0, n_i0 = 0, n_tb = 0, n_te = 0;
+  int n_u = 0, n_jt = 0, n_bh0 = 0, n_i0 = 0, n_hc = 0, n_rev = 0, n_tb = 0, n_te = 0;
   size_t n_base = 0;
   bool has_next = false;
   auto set_item = [&](const KItem& it) __attribute__((always_inline)) {
@@ -738,6 +758,8 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     jt = it.jt;
     bh0 = it.bh0;
     i0 = it.i0;
+    hc = it.hc;
+    rev = it.rev;
     tb = it.tb;
     te = it.te;
     base = it.base;
@@ -745,7 +767,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     n = k0w + c;                // this lane's key
     active = k0w < S;           // wave-uniform
   };
-  set_item(make_item(L0));
+  set_item(make_item(L0, 0));
 
   // K (role 0) or V (role 1) rows as B operands: k-step t holds X[n][16t + 8hh .. +7]
   u32x4 xf[KT];
@@ -773,34 +795,42 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   auto bufp = [&](int t) __attribute__((always_inline)) {
     return bufs + __builtin_amdgcn_readfirstlane(((t + boff) % NBUF) * BUFA);
   };
-  // pair p of item it: query tile i0 + p / G of query head bh0 + p % G; its DMA in
-  // 2 NDMA + 1 parts: part 2x / 2x+1 = block x of the Q / dO tile, part 2 NDMA =
-  // the row-term slice (waves 0 and 1)
+  // position p of an item (chunk ihc, direction irev, te = it): walk index w, i.e.
+  // query tile i0 + w / G of query head bh0 + w % G (without WALK, w = p)
+  auto walk_w = [&](int p, int ihc, int irev, int it) __attribute__((always_inline)) {
+    if constexpr (WALK) return ihc + (irev ? it - 1 - p : p) * nsplit;
+    else return p;
+  };
+  auto qtile = [&](int p) __attribute__((always_inline)) { return i0 + walk_w(p, hc, rev, te) / G; };
+  // the pair's DMA in 2 NDMA + 1 parts: part 2x / 2x+1 = block x of the Q / dO tile,
+  // part 2 NDMA = the row-term slice (waves 0 and 1)
   struct Dma {
     __amdgpu_buffer_rsrc_t q, d, r;
     unsigned char* buf;
   };
-  auto dma_prep = [&](int bh0, int qi0, int p, unsigned char* buf) __attribute__((always_inline)) {
-    const int di = qi0 + p / G, dg = p % G;
-    const size_t row0 = (size_t)(bh0 + dg) * S + (size_t)di * BMQ;
+  auto dma_prep = [&](int dbh, int qi0, int w, unsigned char* buf) __attribute__((always_inline)) {
+    const int di = qi0 + w / G, dg = w % G;
+    const size_t row0 = (size_t)(dbh + dg) * S + (size_t)di * BMQ;
     const int rows = min(BMQ, S - di * BMQ);
     Dma j{make_rsrc(Q + row0 * D, rows * ROWB), make_rsrc(dO + row0 * D, rows * ROWB),
           make_rsrc(Rb + (wave == 1 ? (size_t)B * H * S : 0) + row0, rows * 4), buf};
     return j;
   };
   // the pair at position p of the current item's sequence, continued into the next
-  // item's first two pairs (false: none)
-  auto dma_at = [&](int p, int& dbh0, int& qi0, int& pp) __attribute__((always_inline)) {
+  // item's first two pairs (false: none): walk index w of the item with query heads
+  // from dbh and diagonal tile qi0
+  auto dma_at = [&](int p, int& dbh, int& qi0, int& w) __attribute__((always_inline)) {
     if (p < te) {
-      dbh0 = bh0;
+      dbh = bh0;
       qi0 = i0;
-      pp = p;
+      w = walk_w(p, hc, rev, te);
       return true;
     }
     if (!has_next) return false;
-    dbh0 = n_bh0;
+    dbh = n_bh0;
     qi0 = n_i0;
-    pp = n_tb + (p - te);
+    const int pp = n_tb + (p - te);
+    w = walk_w(pp, n_hc, n_rev, n_te);
     return pp < n_te;
   };
   auto dma_part = [&](const Dma& j, int k) __attribute__((always_inline)) {
@@ -811,8 +841,8 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
       dma4(j.r, j.buf + OFF_L + wave * 4 * BMQ, 4 * lane, 0);
     }
   };
-  auto dma_pair = [&](int bh0, int qi0, int p, unsigned char* buf) __attribute__((always_inline)) {
-    const Dma j = dma_prep(bh0, qi0, p, buf);
+  auto dma_pair = [&](int dbh, int qi0, int w, unsigned char* buf) __attribute__((always_inline)) {
+    const Dma j = dma_prep(dbh, qi0, w, buf);
 #pragma unroll
     for (int k = 0; k <= 2 * NDMA; ++k) dma_part(j, k);
   };
@@ -843,7 +873,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   };
   // query block qb of pair t meets this wave's keys (wave-uniform)
   auto live = [&](int t, int qb) __attribute__((always_inline)) {
-    return active && (i0 + t / G) * BMQ + 32 * qb + 31 >= k0w;
+    return active && qtile(t) * BMQ + 32 * qb + 31 >= k0w;
   };
 
   // front(t): S - LSE/c (role 0) or dP - Delta (role 1) of pair t's two query
@@ -853,7 +883,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   auto front = [&](int t, f32x16 (&x)[2], u32x4 (&pk)[2][2], auto full) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full)::value;
     const unsigned char* buf = bufp(t);
-    const int qrow0 = (i0 + t / G) * BMQ;
+    const int qrow0 = qtile(t) * BMQ;
     const bool l0 = FULL || live(t, 0), l1 = FULL || live(t, 1);
     if (!l1) return;  // (l0 implies l1)
     x[1] = load_rows(reinterpret_cast<const float*>(buf + lo), 1);
@@ -927,11 +957,22 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     }
   };
 
-  // pairs before TE meet this workgroup's keys (edge tests, the diagonal mask);
-  // the rest lie wholly past them.  Only the last key tile can have inactive waves,
-  // and it meets at most two query tiles (NI <= 2), so the full paths need no
-  // activity test.
-  int TE = G * min(2, nq - i0);
+  // positions [0, E0) and [E1, te) hold the pairs of query tiles i0 and i0 + 1, which
+  // meet this workgroup's keys (edge tests, the diagonal mask); [E0, E1) lie wholly
+  // past them.  Only the last key tile can have inactive waves, and it meets at most
+  // two query tiles (NI <= 2), so the full paths need no activity test.
+  int E0 = 0, E1 = 0;
+  auto set_edges = [&]() __attribute__((always_inline)) {
+    const int TEw = G * min(2, nq - i0);                // walk indices of the edge pairs
+    if constexpr (WALK) {
+      const int ne = TEw > hc ? (TEw - hc + nsplit - 1) / nsplit : 0;
+      E0 = rev ? 0 : ne;
+      E1 = rev ? te - ne : te;
+    } else {
+      E0 = min(te, TEw);
+      E1 = te;
+    }
+  };
   // pair t+1 has landed, P(t) is visible, and nobody reads pair t-1's buffer or
   // slot (t+1) % 2 any more
   auto sync = [&]() __attribute__((always_inline)) {
@@ -984,8 +1025,8 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x16{};
     if (tb >= te) return;  // (a chunk of a light key tile can be empty: it stores zeros)
-    if (!(pre & 1)) dma_pair(bh0, i0, tb, bufp(tb));
-    if (tb + 1 < te && !(pre & 2)) dma_pair(bh0, i0, tb + 1, bufp(tb + 1));
+    if (!(pre & 1)) dma_pair(bh0, i0, walk_w(tb, hc, rev, te), bufp(tb));
+    if (tb + 1 < te && !(pre & 2)) dma_pair(bh0, i0, walk_w(tb + 1, hc, rev, te), bufp(tb + 1));
     if (first && tb + 1 < te) {
       // pair tb has landed once at most pair tb+1's operations are outstanding
       if (wave < 2) __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA + 1));
@@ -994,7 +1035,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
       __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
     }
     __syncthreads();
-    if (tb >= TE) front(tb, x, pk, BTag<true>{});
+    if (tb >= E0 && tb < E1) front(tb, x, pk, BTag<true>{});
     else front(tb, x, pk, BTag<false>{});
   };
   // Full pairs with a next pair run as one stream of 32 MFMAs per wave, operand
@@ -1127,16 +1168,18 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     const int Ln = item_L(k + 1);
     has_next = Ln >= 0;
     if (has_next) {
-      const KItem it = make_item(Ln);
+      const KItem it = make_item(Ln, k + 1);
       n_u = it.u;
       n_jt = it.jt;
       n_bh0 = it.bh0;
       n_i0 = it.i0;
+      n_hc = it.hc;
+      n_rev = it.rev;
       n_tb = it.tb;
       n_te = it.te;
       n_base = it.base;
     }
-    TE = G * min(2, nq - i0);
+    set_edges();
     prologue();
   };
   // to the next item: its first pair at position te is in flight if iteration te - 2
@@ -1147,7 +1190,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     xf_pre = te - tb >= 1;
     boff = ((boff + te - n_tb) % NBUF + NBUF) % NBUF;
     first = false;
-    set_item(KItem{n_u, n_jt, n_bh0, n_i0, n_tb, n_te, n_base});
+    set_item(KItem{n_u, n_jt, n_bh0, n_i0, n_hc, n_rev, n_tb, n_te, n_base});
   };
 
   // The two roles run separate loops with the same barriers per item, so each keeps
@@ -1159,51 +1202,50 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
       if (t + 1 < te) front(t + 1, x, pn, full);
       back(t, x, pc, full);
     };
+    auto step_mv = [&](int t, auto full) __attribute__((always_inline)) {
+      step(t, pk, pkn, full);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
+    };
     for (int k = 0;; ++k) {
       begin_item(k);
+      // (E1f: the full pairs whose successor, if any, is full as well)
+      const int E1f = (WALK && E1 < te) ? E1 - 1 : E1;
       int t = tb;
-      for (; t < min(te, TE); ++t) {  // edge pairs: at most two per K/V head
-        step(t, pk, pkn, BTag<false>{});
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
-      }
-      for (; t + 2 < te; t += 2) {
+      for (; t < E0; ++t) step_mv(t, BTag<false>{});  // leading edge pairs
+      for (; t + 2 < E1; t += 2) {
         sync();
         stream0(t, pk, pkn);
         sync();
         stream0(t + 1, pkn, pk);
       }
-      for (; t < te; ++t) {
-        step(t, pk, pkn, BTag<true>{});
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int i1 = 0; i1 < 2; ++i1) pk[qb][i1] = pkn[qb][i1];
-      }
+      for (; t < E1f; ++t) step_mv(t, BTag<true>{});
+      if constexpr (WALK)
+        for (; t < te; ++t) step_mv(t, BTag<false>{});  // trailing edge pairs
       epilogue();
       if (!has_next) break;
       next_item();
     }
   } else {
+    auto step1 = [&](int t, auto full) __attribute__((always_inline)) {
+      top(t);
+      back(t, x, pk, full);
+      if (t + 1 < te) front(t + 1, x, pkn, full);
+    };
     for (int k = 0;; ++k) {
       begin_item(k);
+      const int E1f = (WALK && E1 < te) ? E1 - 1 : E1;
       int t = tb;
-      for (; t < min(te, TE); ++t) {
-        top(t);
-        back(t, x, pk, BTag<false>{});
-        if (t + 1 < te) front(t + 1, x, pkn, BTag<false>{});
-      }
-      for (; t + 1 < te; ++t) {
+      for (; t < E0; ++t) step1(t, BTag<false>{});
+      for (; t + 1 < E1; ++t) {
         sync();
         stream1(t);
       }
-      for (; t < te; ++t) {
-        top(t);
-        back(t, x, pk, BTag<true>{});
-        if (t + 1 < te) front(t + 1, x, pkn, BTag<true>{});
-      }
+      for (; t < E1f; ++t) step1(t, BTag<true>{});
+      if constexpr (WALK)
+        for (; t < te; ++t) step1(t, BTag<false>{});
       epilogue();
       if (!has_next) break;
       next_item();
@@ -1567,10 +1609,16 @@ static bool launch_dkdv(const BwdArgs& a) {
   bool paired = false;
   if constexpr (FA_DKDV_PAIR && D == 128) {
     if (a.rowb) {
-      // one workgroup per CU walks the key tiles (the kernel reads the grid size)
-      const auto kern = dkdv_pair_kernel<E, D, BMQ, BNK>;
-      static const int per_cu = occupancy_per_cu((const void*)kern, 4 * BNK);  // (thread-safe init)
-      const dim3 pgrid(resident_grid((int)grid.x, per_cu));
+      // one workgroup per CU walks the key tiles (the kernel reads the grid size); the
+      // alternating walk when a K/V head's query heads of Q and dO exceed the 4 MiB L2
+      // (backward against the upward walk, D = 128 bf16: B=2 H=32 S=4096 with G = 4
+      // +3.9 %, B=1 H=32 S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %; with G = 1
+      // (B=4) and G = 2 (4 MiB) it measured -1.8 and -1.2 %)
+      const bool walk = (long long)(a.H / a.Hkv) * a.S * D * 4 > (4ll << 20);
+      const auto kern = walk ? dkdv_pair_kernel<E, D, BMQ, BNK, true> : dkdv_pair_kernel<E, D, BMQ, BNK, false>;
+      static const int per_cu_up = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, false>, 4 * BNK);
+      static const int per_cu_walk = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, true>, 4 * BNK);
+      const dim3 pgrid(resident_grid((int)grid.x, walk ? per_cu_walk : per_cu_up));
       hipLaunchKernelGGL(kern, pgrid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
                          (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.d_o,
                          a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,

@@ -187,3 +187,31 @@ def test_dkdv_split_matches_register_sums(shape):
         assert torch.equal(out[0], ref[0])
         for g, r in zip(out[1:], ref[1:]):
             assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 1, 1100, 128), (1, 16, 2, 2049, 128), (2, 8, 2, 3000, 128)],
+                         ids=lambda s: "B%dH%dHkv%dS%dD%d" % s)
+def test_dkdv_alternating_walk(shape):
+    """Shapes whose K/V heads' query heads of Q and dO exceed 4 MiB take the dK/dV walk whose even
+    rounds run from the last query tile down, with the split's chunks interleaved (partial last
+    tiles, splits of 57, 16 and 6 chunks here; the unsplit walk is the full-size B2 H32 Hkv8 case):
+    against the fp32 reference, against one workgroup summing each key tile's pairs in registers
+    (no workspace), with a smaller split, and bitwise reproducible."""
+    from attention import _lib
+    from attention.backward.fused_backward import _forward
+    B, H, Hkv, S, D = shape
+    assert (H // Hkv) * S * D * 4 > 4 << 20
+    q, k, v, do = make(B, H, Hkv, S, D, torch.bfloat16, seed=S + H)
+    log(f"dkdv alternating walk {shape}")
+    check(q, k, v, do, (128, 64), f"dkdv walk {shape}")
+    o, lse = _forward(q, k, v, 128, 64)
+    need = _lib.load().fa_bwd_gqa_workspace_size(B, H, Hkv, S, D)
+    ref = _bwd_through_abi(q, k, v, o, do, lse, 0)
+    got = _bwd_through_abi(q, k, v, o, do, lse, need)
+    half = _bwd_through_abi(q, k, v, o, do, lse, need // 2)
+    for out in (got, half):
+        assert torch.equal(out[0], ref[0])
+        for g, r in zip(out[1:], ref[1:]):
+            assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
+    again = _bwd_through_abi(q, k, v, o, do, lse, need)
+    assert all(torch.equal(a, b) for a, b in zip(got, again))
