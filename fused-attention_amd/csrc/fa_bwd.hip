@@ -957,9 +957,9 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     }
   };
 
-  // positions [0, E0) and [E1, te) hold the pairs of query tiles i0 and i0 + 1, which
-  // meet this workgroup's keys (edge tests, the diagonal mask); [E0, E1) lie wholly
-  // past them.  Only the last key tile can have inactive waves, and it meets at most
+  // positions [tb, E0) and [E1, te) hold the pairs of query tiles i0 and i0 + 1, which
+  // meet this workgroup's keys (edge tests, the diagonal mask); [max(tb, E0), E1) lie
+  // wholly past them.  Only the last key tile can have inactive waves, and it meets at most
   // two query tiles (NI <= 2), so the full paths need no activity test.
   int E0 = 0, E1 = 0;
   auto set_edges = [&]() __attribute__((always_inline)) {
