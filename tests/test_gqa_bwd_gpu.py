@@ -189,19 +189,20 @@ def test_dkdv_split_matches_register_sums(shape):
             assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
 
 
-@pytest.mark.parametrize("shape", [(1, 8, 1, 1100, 128), (1, 16, 2, 2049, 128), (2, 8, 2, 3000, 128)],
-                         ids=lambda s: "B%dH%dHkv%dS%dD%d" % s)
+@pytest.mark.parametrize("shape", [(1, 8, 1, 1100, 128, "bf16"), (1, 16, 2, 2049, 128, "bf16"),
+                                   (2, 8, 2, 3000, 128, "bf16"), (1, 8, 1, 1100, 128, "fp16")],
+                         ids=lambda s: "B%dH%dHkv%dS%dD%d-%s" % s)
 def test_dkdv_alternating_walk(shape):
     """Shapes whose K/V heads' query heads of Q and dO exceed 4 MiB take the dK/dV walk whose even
     rounds run from the last query tile down, with the split's chunks interleaved (partial last
-    tiles, splits of 57, 16 and 6 chunks here; the unsplit walk is the full-size B2 H32 Hkv8 case):
-    against the fp32 reference, against one workgroup summing each key tile's pairs in registers
+    tiles, splits of 57, 16 and 6 chunks here, bf16 and fp16; the unsplit walk is the full-size
+    B2 H32 Hkv8 case): against the fp32 reference, against one workgroup summing each key tile's pairs in registers
     (no workspace), with a smaller split, and bitwise reproducible."""
     from attention import _lib
     from attention.backward.fused_backward import _forward
-    B, H, Hkv, S, D = shape
+    B, H, Hkv, S, D, dt = shape
     assert (H // Hkv) * S * D * 4 > 4 << 20
-    q, k, v, do = make(B, H, Hkv, S, D, torch.bfloat16, seed=S + H)
+    q, k, v, do = make(B, H, Hkv, S, D, DTYPES[dt], seed=S + H)
     log(f"dkdv alternating walk {shape}")
     check(q, k, v, do, (128, 64), f"dkdv walk {shape}")
     o, lse = _forward(q, k, v, 128, 64)
