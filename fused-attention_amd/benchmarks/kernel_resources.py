@@ -60,6 +60,20 @@ def parse(text):
     return kernels
 
 
+HEADER = [
+    "# Registers, LDS, scratch and occupancy of every kernel instance (compiler report, gfx950)",
+    "",
+    "    cd fused-attention_amd && python3 -m benchmarks.kernel_resources --out ../profiles/kernel_resources.md",
+    "",
+    "Each slice of `csrc/` compiled as the Makefile does with `-Rpass-analysis=kernel-resource-usage`;",
+    "\"Occupancy\" is the compiler's waves per SIMD for the registers and LDS.  Template arguments:",
+    "`fwd_kernel<E, D, rows per head, keys per tile, heads per workgroup, LSE>`,",
+    "`dq_kernel<E, D, rows, keys>`, `dkdv_kernel<E, D, query rows per tile, keys per workgroup, per-row terms>`,",
+    "`dkdv_pair_kernel<E, D, query rows per tile, keys per workgroup, alternating walk>` (D = 128 only).",
+    "",
+]
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--hipcc", default="/opt/rocm/bin/hipcc")
@@ -68,7 +82,7 @@ def main(argv=None):
     jobs = [(f, e, d) for f in ("fwd", "bwd") for e, d in SLICES]
     with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         results = list(ex.map(lambda j: compile_slice(args.hipcc, *j), jobs))
-    L = ["| kernel | " + " | ".join(FIELDS) + " |", "|---|" + "---|" * len(FIELDS)]
+    L = HEADER + ["| kernel | " + " | ".join(FIELDS) + " |", "|---|" + "---|" * len(FIELDS)]
     for kernels in results:
         for name in sorted(kernels, key=demangle):
             k = kernels[name]
