@@ -216,3 +216,26 @@ def test_dkdv_alternating_walk(shape):
             assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
     again = _bwd_through_abi(q, k, v, o, do, lse, need)
     assert all(torch.equal(a, b) for a, b in zip(got, again))
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 1, 2200), (3, 8, 2, 2500), (1, 32, 2, 700), (2, 24, 3, 1500),
+                                   (1, 64, 1, 200), (1, 2, 1, 8193), (1, 1, 1, 9000), (4, 16, 4, 2100)],
+                         ids=lambda s: "B%dH%dHkv%dS%d" % s)
+def test_dkdv_alternating_walk_sweep(shape):
+    """More shapes of the alternating dK/dV walk (D = 128 bf16, G from 1 to 64, S from 200 to 9000,
+    splits of 2 to 64 chunks): equal to one workgroup summing each key tile's pairs in registers up
+    to fp32 summation order, dQ identical."""
+    from attention import _lib
+    from attention.backward.fused_backward import _forward
+    B, H, Hkv, S = shape
+    D = 128
+    assert (H // Hkv) * S * D * 4 > 4 << 20
+    q, k, v, do = make(B, H, Hkv, S, D, torch.bfloat16, seed=7 * S + H)
+    log(f"dkdv alternating walk sweep {shape}")
+    o, lse = _forward(q, k, v, 128, 64)
+    need = _lib.load().fa_bwd_gqa_workspace_size(B, H, Hkv, S, D)
+    ref = _bwd_through_abi(q, k, v, o, do, lse, 0)
+    got = _bwd_through_abi(q, k, v, o, do, lse, need)
+    assert torch.equal(got[0], ref[0])
+    for g, r in zip(got[1:], ref[1:]):
+        assert float((g.float() - r.float()).abs().max()) <= 2e-2 + 1e-2 * float(r.float().abs().max())
