@@ -1610,11 +1610,12 @@ static bool launch_dkdv(const BwdArgs& a) {
   if constexpr (FA_DKDV_PAIR && D == 128) {
     if (a.rowb) {
       // one workgroup per CU walks the key tiles (the kernel reads the grid size); the
-      // alternating walk when a K/V head's query heads of Q and dO exceed the 4 MiB L2
+      // alternating walk when a K/V head's query heads of Q and dO fill the 4 MiB L2
       // (backward against the upward walk, D = 128 bf16: B=2 H=32 S=4096 with G = 4
-      // +3.9 %, B=1 H=32 S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %; with G = 1
-      // (B=4) and G = 2 (4 MiB) it measured -1.8 and -1.2 %)
-      const bool walk = (long long)(a.H / a.Hkv) * a.S * D * 4 > (4ll << 20);
+      // +3.9 %, B=1 H=32 S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %, MHA
+      // S=8192 B=2 H=32 / B=1 H=32 / B=1 H=16 +3.2 / +3.6 / +1.8 %, G = 2 S=4096
+      // B=2 / B=1 / B=4 H=32 +0.0 / +0.6 / +0.5 %; MHA S=4096 (2 MiB) B=4 H=32 -1.8 %)
+      const bool walk = (long long)(a.H / a.Hkv) * a.S * D * 4 >= (4ll << 20);
       const auto kern = walk ? dkdv_pair_kernel<E, D, BMQ, BNK, true> : dkdv_pair_kernel<E, D, BMQ, BNK, false>;
       static const int per_cu_up = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, false>, 4 * BNK);
       static const int per_cu_walk = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, true>, 4 * BNK);
