@@ -224,8 +224,8 @@ def test_dkdv_alternating_walk(shape):
                          ids=lambda s: "B%dH%dHkv%dS%d" % s)
 def test_dkdv_alternating_walk_sweep(shape):
     """More shapes of the alternating dK/dV walk (D = 128 bf16, G from 1 to 64, S from 200 to 9000,
-    splits of 2 to 64 chunks, the 4 MiB threshold itself): equal to one workgroup summing each key tile's pairs in registers up
-    to fp32 summation order, dQ identical."""
+    splits of 2 to 64 chunks, the 4 MiB threshold itself): equal to one workgroup summing each key
+    tile's pairs in registers up to fp32 summation order, dQ identical."""
     from attention import _lib
     from attention.backward.fused_backward import _forward
     B, H, Hkv, S = shape
