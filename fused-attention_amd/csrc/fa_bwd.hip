@@ -1614,7 +1614,7 @@ static bool launch_dkdv(const BwdArgs& a) {
       // (backward against the upward walk, D = 128 bf16: B=2 H=32 S=4096 with G = 4
       // +3.9 %, B=1 H=32 S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %, MHA
       // S=8192 B=2 H=32 / B=1 H=32 / B=1 H=16 +3.2 / +3.6 / +1.8 %, G = 2 S=4096
-      // B=2 / B=1 / B=4 H=32 +0.0 / +0.6 / +0.5 %; MHA S=4096 (2 MiB) B=4 H=32 -1.8 %)
+      // B=2 / B=1 / B=4 H=32 +0.0 / +0.6 / +0.5 %; MHA S=4096 (2 MiB) B=4 H=32 -1.0 / -1.1 %)
       const bool walk = (long long)(a.H / a.Hkv) * a.S * D * 4 >= (4ll << 20);
       const auto kern = walk ? dkdv_pair_kernel<E, D, BMQ, BNK, true> : dkdv_pair_kernel<E, D, BMQ, BNK, false>;
       static const int per_cu_up = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, false>, 4 * BNK);
