@@ -697,7 +697,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   // di >= i0 (its diagonal tile) of the G query heads bh0 + dg.  Without WALK, chunk hc
   // is the range [T hc / nsplit, T (hc+1) / nsplit) of the T = G (nq - i0) indices,
   // run upward from the diagonal.  With WALK (chosen when a K/V head's G heads of Q
-  // and dO exceed the L2), chunk hc takes the w with w % nsplit == hc, and items of
+  // and dO fill the L2), chunk hc takes the w with w % nsplit == hc, and items of
   // even rounds run their chunk from the last query tile down, odd rounds from the
   // diagonal up: the slots of an XCD all start an even round at the last query tile,
   // and each starts its odd-round item (diagonal two tiles below where its even-round
@@ -795,10 +795,10 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   auto bufp = [&](int t) __attribute__((always_inline)) {
     return bufs + __builtin_amdgcn_readfirstlane(((t + boff) % NBUF) * BUFA);
   };
-  // position p of an item (chunk ihc, direction irev, te = it): walk index w, i.e.
-  // query tile i0 + w / G of query head bh0 + w % G (without WALK, w = p)
-  auto walk_w = [&](int p, int ihc, int irev, int it) __attribute__((always_inline)) {
-    if constexpr (WALK) return ihc + (irev ? it - 1 - p : p) * nsplit;
+  // position p of an item (chunk ihc, direction irev, positions 0 .. ite-1): walk
+  // index w, i.e. query tile i0 + w / G of query head bh0 + w % G (without WALK, w = p)
+  auto walk_w = [&](int p, int ihc, int irev, int ite) __attribute__((always_inline)) {
+    if constexpr (WALK) return ihc + (irev ? ite - 1 - p : p) * nsplit;
     else return p;
   };
   auto qtile = [&](int p) __attribute__((always_inline)) { return i0 + walk_w(p, hc, rev, te) / G; };
