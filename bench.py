@@ -85,20 +85,27 @@ def device_warmup(fn, seconds, torch):
 
 
 def time_steps(fn, steps, warmup, torch, warm_seconds):
-    """Per-step event timing on the current (launch) stream, plus wall time of the whole run."""
+    """Wall time of `steps` back-to-back steps between two device synchronisations (nothing
+    else on the stream in between), then the same number of steps again with an event pair
+    around each on the current (launch) stream, for the mean and median step duration on
+    the device.  The events go in a pass of their own: each one is a packet of its own in
+    the queue, and the device time they add between kernels is not part of the work."""
     device_warmup(fn, warm_seconds, torch)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
     stream = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    t0 = time.perf_counter()
     for a, b in evs:
         a.record(stream)
         fn()
         b.record(stream)
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
     per = [a.elapsed_time(b) for a, b in evs]
     return wall_ms / steps, statistics.mean(per), statistics.median(per)
 
