@@ -74,23 +74,8 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
   return FA_OK;
 }
 
-// CU count of the current device, read once per device: the launch paths ask on
-// every call, and a short call is bound by host time.
-constexpr int kMaxDevices = 64;
-std::atomic<int> g_cus[kMaxDevices];
-int cu_count() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
-  int cus = (dev >= 0 && dev < kMaxDevices) ? g_cus[dev].load(std::memory_order_relaxed) : 0;
-  if (cus <= 0) {
-    if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    else if (dev < kMaxDevices)
-      g_cus[dev].store(cus, std::memory_order_relaxed);
-  }
-  return cus;
-}
+using fa::cu_count;
+using fa::kMaxDevices;
 
 // Forward query heads per workgroup for this launch: heads_per_wg's choice, but
 // four heads (64-row tiles) drop to two when the grid would hold fewer than four
@@ -276,11 +261,13 @@ int fa_bwd_gqa_noalloc(const void* q, const void* k, const void* v, const void* 
   if (st != FA_OK) return st;
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
-  // the workspace fa_bwd_gqa would take for this shape must fit the scratch whole: the
-  // same per-row terms and the same split, hence the same kernels and the same results.
-  // Nothing in it needs clearing: dQ writes every row's terms before dK/dV reads them,
-  // and every split chunk stores its whole partial sum before the reduction reads it.
-  if (fa_bwd_gqa_workspace_size(B, H, H_kv, S, D) > kNoAllocScratchBytes) return FA_ERR_SCRATCH;
+  // the scratch is fa_bwd_gqa's workspace of kNoAllocScratchBytes: the per-row terms must
+  // fit, and fa_bwd_gqa then takes the largest dK/dV split whose partial sums fit behind
+  // them (the whole split the shape asks for when it fits), so the results are those of
+  // fa_bwd_gqa given a workspace of that size.  Nothing in it needs clearing: dQ writes
+  // every row's terms before dK/dV reads them, and every split chunk stores its whole
+  // partial sum before the reduction reads it.
+  if (rowb_bytes(B, H, S) > kNoAllocScratchBytes) return FA_ERR_SCRATCH;
   void* ws = nullptr;
   st = scratch_address(&ws);
   if (st != FA_OK) return st;
@@ -369,10 +356,11 @@ const char* fa_strerror(int status) {
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_LAUNCH: return "HIP kernel launch failed";
     case FA_ERR_UNSUPPORTED: return "no kernel for this combination";
-    case FA_ERR_WORKSPACE: return "workspace not 16-byte aligned";
+    case FA_ERR_WORKSPACE:
+      return "workspace not 16-byte aligned (or, for fa_bwd_gqa_exact, too small for the requested split)";
     case FA_ERR_SCRATCH:
-      return "this shape needs more workspace than the library's device scratch (fa_bwd_gqa_noalloc); "
-             "use fa_bwd_gqa with a caller workspace";
+      return "this shape's per-row terms (8 * B * H * S bytes) exceed the library's device scratch "
+             "(fa_bwd_gqa_noalloc); use fa_bwd_gqa with a caller workspace";
     default: return "unknown status";
   }
 }

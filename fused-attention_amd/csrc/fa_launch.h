@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include "../../include/fa.h"
 
 namespace fa {
@@ -57,30 +59,38 @@ inline bool smem_attr(const void* kern) {
   return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, SMEM) == hipSuccess;
 }
 
+// CU count of the current device, read once per device and kept (the launch paths ask
+// on every call, and a short call is bound by host time).  A failed query is answered
+// with 256 (an MI355X) and leaves the HIP error state as the query left it: nothing here
+// clears an error the caller's own work left behind.
+constexpr int kMaxDevices = 64;
+inline int cu_count() {
+  static std::atomic<int> cus_of[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int cus = cus_of[dev].load(std::memory_order_relaxed);
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  cus_of[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
 // Grid of a kernel whose workgroups walk their share of `items` work items: the item
 // count rounded up to a multiple of 8 (workgroups reach the 8 XCDs in turn), capped
 // at the workgroups the device runs at once (its CUs times the kernel's occupancy
 // per_cu, rounded down to a multiple of 8).
 inline int resident_grid(int items, int per_cu) {
   const int all = (items + 7) / 8 * 8;
-  int dev = 0, cus = 0;
-  if (per_cu <= 0 || hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return all;
-  }
-  const int resident = cus * per_cu / 8 * 8;
+  if (per_cu <= 0) return all;
+  const int resident = cu_count() * per_cu / 8 * 8;
   return resident >= 8 && resident < all ? resident : all;
 }
 
 // Workgroups of `kern` (launched with `threads` threads) that one CU holds at once;
-// 0 if the runtime cannot tell.
+// 0 if the runtime cannot tell (the callers keep the answer per kernel).
 inline int occupancy_per_cu(const void* kern, int threads) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess) {
-    (void)hipGetLastError();
-    return 0;
-  }
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess) return 0;
   return per_cu;
 }
 

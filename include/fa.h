@@ -2,10 +2,13 @@
  * fa.h - C ABI of libfa.so, the MI355X (gfx950) fused causal attention library.
  *
  * Every entry point enqueues work on the caller's HIP stream and returns
- * without synchronising.  The caller owns every buffer (inputs, outputs and
- * LSE); the library allocates no device memory and keeps no pointer after
- * a call returns.  All tensors are dense, row-major [B, heads, S, D] in
- * device memory; LSE is dense [B, H, S] float32.
+ * without synchronising.  The caller owns every buffer (inputs, outputs, LSE
+ * and the backward's workspace); no call allocates device memory, and none
+ * keeps a pointer after it returns.  The library does hold one static device
+ * array: the 64 MiB scratch behind fa_bwd_gqa_noalloc, which every device the
+ * loaded library runs on carries (in its code object's memory) until the
+ * process ends, whichever entry points a caller uses.  All tensors are dense,
+ * row-major [B, heads, S, D] in device memory; LSE is dense [B, H, S] float32.
  *
  * Return value: FA_OK (0) or one of the negative FA_ERR_* codes below.
  * fa_strerror() turns a code into a static message.
@@ -37,8 +40,9 @@ enum fa_status {
   FA_ERR_NULL = -5,     /* a required pointer is NULL */
   FA_ERR_LAUNCH = -6,   /* the HIP runtime rejected a launch */
   FA_ERR_UNSUPPORTED = -7, /* valid arguments, but no kernel for this combination */
-  FA_ERR_WORKSPACE = -8,   /* fa_bwd_gqa: workspace not 16-byte aligned */
-  FA_ERR_SCRATCH = -9      /* fa_bwd_gqa_noalloc: shape needs more than the library's scratch */
+  FA_ERR_WORKSPACE = -8,   /* fa_bwd_gqa*: workspace not 16-byte aligned; fa_bwd_gqa_exact:
+                              also a workspace too small for the requested split */
+  FA_ERR_SCRATCH = -9      /* fa_bwd_gqa_noalloc: the per-row terms exceed the library's scratch */
 };
 
 /*
@@ -122,15 +126,15 @@ FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o
 /*
  * fa_bwd_gqa for callers that cannot allocate device memory -- code under HIP graph
  * capture, serving loops and harnesses that forbid hipMalloc.  No counterpart in the
- * reference.  Same arguments and results as fa_bwd_gqa(..., workspace, bytes, stream)
- * given a workspace of fa_bwd_gqa_workspace_size() bytes (bitwise: the same kernels
- * with the same split), but the workspace is the library's own device scratch, a
- * static array of fa_noalloc_scratch_bytes() = 64 MiB that each device holds from the
- * library's first use on it until the process ends.  The call allocates nothing (no
- * hipMalloc, no hipFree, no allocating library routine).
- *   Limit: shapes whose fa_bwd_gqa_workspace_size() exceeds 64 MiB are rejected with
- *   FA_ERR_SCRATCH before anything is enqueued (8 * B * H * S bytes of per-row terms,
- *   plus the split's partial sums: e.g. B * H * S <= 8M with no split).
+ * reference.  Same arguments as fa_bwd_gqa, and the results of
+ * fa_bwd_gqa(..., workspace, fa_noalloc_scratch_bytes(), stream) bitwise: the workspace
+ * is the library's own device scratch, a static array of fa_noalloc_scratch_bytes() =
+ * 64 MiB that each device holds from the library's first use on it until the process
+ * ends.  The per-row terms come first; the dK/dV split is the one the shape asks for
+ * when its partial sums fit behind them, else the largest that fits (possibly none).
+ * The call allocates nothing (no hipMalloc, no hipFree, no allocating library routine).
+ *   Limit: shapes whose per-row terms (8 * B * H * S bytes, i.e. B * H * S above 8M
+ *   rows) exceed 64 MiB are rejected with FA_ERR_SCRATCH before anything is enqueued.
  *   Every call on a device shares that device's scratch: calls whose work overlaps on
  *   one device (different streams, or host threads without ordering) race; serialise
  *   them on one stream.  Nothing in the scratch needs to start at zero.

@@ -174,7 +174,9 @@ def test_no_unresolved_library_symbols():
 
 def test_noalloc_entry_rejects_shapes_past_its_scratch(lib):
     """fa_bwd_gqa_noalloc: argument errors as fa_bwd_gqa, and FA_ERR_SCRATCH -- before any
-    launch -- when the shape's workspace exceeds the library's 64 MiB device scratch."""
+    launch -- when the shape's per-row terms (8 * B * H * S bytes) exceed the library's 64 MiB
+    device scratch.  A shape whose full dK/dV split would not fit behind them is accepted
+    and runs a smaller split (tests/test_zz_no_alloc.py, on the GPU)."""
     assert lib.fa_noalloc_scratch_bytes() == 64 << 20
 
     def noalloc(B=1, H=4, Hkv=2, S=256, D=64, dtype=1, bm=64, bn=64, ptr=FAKE):
@@ -186,13 +188,9 @@ def test_noalloc_entry_rejects_shapes_past_its_scratch(lib):
     assert noalloc(bn=32) == _lib.FA_ERR_TILE
     assert noalloc(ptr=NULL) == _lib.FA_ERR_NULL
     assert noalloc(S=1 << 25, D=32, H=1, Hkv=1) == _lib.FA_ERR_DIMS
-    # 8 * B * H * S bytes of per-row terms alone: 4 * 32 * 65537 rows > 8M
-    assert lib.fa_bwd_gqa_workspace_size(4, 32, 32, 65537, 64) > lib.fa_noalloc_scratch_bytes()
+    # 4 * 32 * 65537 rows: 67,109,888 bytes of per-row terms, one row past the 8M that fit
     assert noalloc(B=4, H=32, Hkv=32, S=65537) == _lib.FA_ERR_SCRATCH
-    # a split that would not fit: MQA with few key tiles asks for large fp32 partial sums
-    big = lib.fa_bwd_gqa_workspace_size(1, 32, 1, 16384, 128)
-    assert big > lib.fa_noalloc_scratch_bytes()
-    assert noalloc(B=1, H=32, Hkv=1, S=16384, D=128) == _lib.FA_ERR_SCRATCH
+    assert noalloc(B=4, H=32, Hkv=32, S=65537, D=128) == _lib.FA_ERR_SCRATCH
     assert "scratch" in lib.fa_strerror(_lib.FA_ERR_SCRATCH).decode()
 
 
