@@ -35,6 +35,23 @@ BWD_COLS = ["test", "B", "H", "N", "D", "sigma", "relerr_O", "relerr_dQ", "reler
             "fused_ms", "sdpa_ms", "fused_speedup_vs_sdpa"]
 
 
+MARGIN_COLS = ["test", "B", "H", "H_kv", "N", "D", "dtype", "tiles", "output", "max_abs_err", "bar",
+               "max_abs_over_bar", "mixed_tol_ratio", "rel_frobenius", "oracle_max_abs"]
+
+
+def margin(test, q, k, tiles, output, max_abs, bar, mixed=None, rel=None, oracle=None):
+    """One row of the full-size workloads' error margins (margins/full_size_margins.csv): the
+    output's max-abs error against the fp32 reference, the bar it is held to, and the other
+    measures its test applies (mixed 2e-2 + 2e-2|ref| ratio, relative Frobenius, oracle)."""
+    B, H, N, D = q.shape
+    fmt = lambda x: "" if x is None else f"{x:.4e}"
+    record("margins/full_size_margins.csv", MARGIN_COLS,
+           dict(test=test, B=B, H=H, H_kv=k.shape[1], N=N, D=D, dtype=str(q.dtype).replace("torch.", ""),
+                tiles=f"{tiles[0]}x{tiles[1]}", output=output, max_abs_err=fmt(max_abs), bar=f"{bar:g}",
+                max_abs_over_bar=f"{max_abs / bar:.3f}", mixed_tol_ratio=fmt(mixed), rel_frobenius=fmt(rel),
+                oracle_max_abs=fmt(oracle)))
+
+
 def record(path, columns, row):
     RECORDS.setdefault((path, tuple(columns)), []).append([row.get(c, "") for c in columns])
 
@@ -88,9 +105,10 @@ def head_samples(B, H):
     return sorted(picks)
 
 
-def check_forward(out, q, k, v, rows_count=40, label="", case=None, tiles=None, seconds=None):
+def check_forward(out, q, k, v, rows_count=40, label="", case=None, tiles=None, seconds=None, margin_test=None):
     """Assert out (GPU) matches the oracle on sampled rows and the fp32 reference everywhere.
-    With `case` (one of the reference's suite cases) the comparison is also recorded."""
+    With `case` (one of the reference's suite cases) the comparison is also recorded; with
+    `margin_test` (a full-size workload) its margin is."""
     B, H, N, D = q.shape
     g = H // k.shape[1]
     ref = cpu_reference.reference_chunked(q, k, v)
@@ -119,6 +137,8 @@ def check_forward(out, q, k, v, rows_count=40, label="", case=None, tiles=None, 
         got = out[b:b + 1, h:h + 1, rows].double().cpu().numpy()
         worst = max(worst, float(np.abs(got - want).max()))
     log(f"{label} max_abs={max_abs:.3e} tol_ratio={ratio:.3f} oracle_rows_max_abs={worst:.3e}")
+    if margin_test is not None:
+        margin(margin_test, q, k, tiles, "O", max_abs, MAX_ABS, mixed=ratio, oracle=worst)
     assert max_abs <= MAX_ABS and ratio <= 1.0, (label, max_abs, ratio)
     assert worst <= MAX_ABS, (label, worst)
     return max_abs, ratio, worst

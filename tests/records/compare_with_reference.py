@@ -82,11 +82,35 @@ def backward_section(ours_glob, ref_path):
     return L + [""]
 
 
+def margins_section(path):
+    """The full-size workloads' error margins (written by the GPU suites; no reference counterpart:
+    the reference records its suites' cases only)."""
+    L = ["## Full-size workloads: error margins", ""]
+    if not os.path.exists(path):
+        return L + ["(no records of this build)", ""]
+    rows = load(path)
+    L += ["Max-abs error of each output against the fp32 reference on every element (the north-star bar "
+          "is 2e-2), its ratio to that bar, and the other measures the test applies: the mixed ratio "
+          "max |x-r| / (2e-2 + 2e-2 |r|) (forward suites, and dK / dV of a K/V group), the relative "
+          "Frobenius error (backward), the float64 oracle's max-abs on sampled heads or rows.", "",
+          "| workload | dtype | tiles | output | max_abs_err | / 2e-2 | mixed ratio | rel. Frobenius | oracle max_abs |",
+          "|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        bar = fnum(r["bar"])
+        L.append(f"| {r['test']} | {r['dtype']} | {r['tiles']} | {r['output']} | {r['max_abs_err']} | "
+                 f"{fnum(r['max_abs_err']) / bar:.3f} | {r['mixed_tol_ratio']} | {r['rel_frobenius']} | "
+                 f"{r['oracle_max_abs']} |" if bar == 2e-2 else
+                 f"| {r['test']} | {r['dtype']} | {r['tiles']} | {r['output']} (bar {r['bar']}) | {r['max_abs_err']} | "
+                 f"{r['max_abs_over_bar']} | | | |")
+    return L + [""]
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--ours", default=os.path.join(REPO, "results", "correctness"))
     p.add_argument("--reference", default="/root/reference/results/correctness")
     p.add_argument("--out", default="")
+    p.add_argument("--commit", default="", help="the commit whose GPU run wrote this build's CSVs")
     a = p.parse_args(argv)
     L = ["# Per-case correctness: this build (MI355X, libfa.so) beside the reference's committed records",
          "", "Reference: its committed CSVs (`results/correctness/fused/v3_occupancy2/*`, "
@@ -96,13 +120,15 @@ def main(argv=None):
          "reference's metrics (`tests/fused/run_correctness.py:33-36,70-80`: max-abs, relative error "
          "floored at 1e-3, tol_ratio = max |o-r| / (2e-2 + 2e-2 |r|); backward: ||x-r|| / ||r||).  "
          "Cases whose N is not a multiple of a tile, which the reference skips, run here with a partial "
-         "last tile.", ""]
+         "last tile." + (f"  This build's CSVs were written by the GPU run of commit {a.commit}." if a.commit else ""),
+         ""]
     L += suite_section("MHA forward suite (84 cases, fp16)", os.path.join(a.ours, "fused", "hip", "*", "*.csv"),
                        os.path.join(a.reference, "fused", "v3_occupancy2", "*", "*.csv"))
     L += suite_section("GQA forward suite (96 cases, fp16)", os.path.join(a.ours, "fused_gqa", "hip", "*", "*.csv"),
                        os.path.join(a.reference, "fused_gqa", "v0_baseline", "*", "*.csv"))
     L += backward_section(os.path.join(a.ours, "backward", "*.csv"),
                           os.path.join(a.reference, "backward", "backward_64x64.csv"))
+    L += margins_section(os.path.join(a.ours, "margins", "full_size_margins.csv"))
     text = "\n".join(L) + "\n"
     if a.out:
         with open(a.out, "w") as f:

@@ -22,7 +22,7 @@ from attention.backward.fused_backward import FusedAttentionFn, fused_attention_
 from oracle import attention_oracle as orc
 from oracle import cases
 from oracle.cpu_reference import reference_grads
-from tests.gpu_util import BWD_COLS, dev, log, record
+from tests.gpu_util import BWD_COLS, dev, log, margin, record
 
 pytestmark = pytest.mark.gpu
 
@@ -40,7 +40,7 @@ def run_fused(q, k, v, do, tiles):
     return o.detach(), q.grad, k.grad, v.grad
 
 
-def check_grads(q, k, v, do, tiles, label, oracle_heads=2, unit_variance=True, case=None):
+def check_grads(q, k, v, do, tiles, label, oracle_heads=2, unit_variance=True, case=None, margin_test=None):
     got = run_fused(q, k, v, do, tiles)
     for name, g in zip(("O", "dQ", "dK", "dV"), got):
         assert g.dtype == q.dtype and g.shape == q.shape, name
@@ -74,6 +74,9 @@ def check_grads(q, k, v, do, tiles, label, oracle_heads=2, unit_variance=True, c
             orc_worst = max(orc_worst, float(e))
     log(f"{label} " + " ".join(f"{n}:abs={a:.2e},rel={r:.1e}" for n, (a, r) in worst.items())
         + f" oracle_max_abs={orc_worst:.2e}")
+    if margin_test is not None:
+        for name, (a, r) in worst.items():
+            margin(margin_test, q, k, tiles, name, a, MAX_ABS, rel=r, oracle=orc_worst)
     for name, (a, r) in worst.items():
         assert r <= REL, (label, name, a, r)
         assert a <= MAX_ABS or not unit_variance, (label, name, a, r)
@@ -106,14 +109,34 @@ def test_backward_small_shapes(dt, D, tiles):
 def test_full_size_fp16_B2_H16_S4096_D64(tiles):
     q, k, v, do = inputs((2, 16, 4096, 64), seed=5, dtype=torch.float16)
     log(f"bwd full-size fp16 D64 tiles={tiles}")
-    check_grads(q, k, v, do, tiles, f"bwd B2H16 S4096 D64 {tiles}", oracle_heads=1)
+    check_grads(q, k, v, do, tiles, f"bwd B2H16 S4096 D64 {tiles}", oracle_heads=1,
+                margin_test="fwd+bwd B2 H16 S4096 D64")
 
 
 @pytest.mark.parametrize("tiles", [(64, 64), (128, 64)], ids=lambda t: f"{t[0]}x{t[1]}")
 def test_full_size_bf16_B4_H32_S4096_D128(tiles):
     q, k, v, do = inputs((4, 32, 4096, 128), seed=6, dtype=torch.bfloat16)
     log(f"bwd full-size bf16 D128 tiles={tiles}")
-    check_grads(q, k, v, do, tiles, f"bwd B4H32 S4096 D128 {tiles}", oracle_heads=1)
+    check_grads(q, k, v, do, tiles, f"bwd B4H32 S4096 D128 {tiles}", oracle_heads=1,
+                margin_test="fwd+bwd B4 H32 S4096 D128")
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 8192, 128), (1, 2, 9000, 128)], ids=lambda s: "x".join(map(str, s)))
+def test_long_sequence_bf16_D128_takes_the_alternating_walk(shape):
+    """MHA at D = 128 whose query head of Q and dO reaches 4 MiB (S >= 8192) runs the paired
+    dK/dV kernel's alternating walk, and with few heads a split of each key tile's pairs; the
+    Python-path backward there against fp32 autograd on every element and the float64 oracle
+    on a head, at max-abs <= 2e-2 (the reference's own published backward length is N = 8192,
+    benchmarks/benchmark_backward.py:107)."""
+    from attention import _lib
+    B, H, S, D = shape
+    lib = _lib.load()
+    assert S * D * 4 >= 4 << 20  # the walk's rule: G * S * D * 4 bytes of Q and dO per K/V head
+    split = lib.fa_bwd_dkdv_split(B, H, H, S)
+    q, k, v, do = inputs(shape, seed=S + H, dtype=torch.bfloat16)
+    log(f"bwd walk MHA bf16 {shape} (dK/dV split {split})")
+    check_grads(q, k, v, do, (64, 64), f"bwd walk {shape} split {split}", oracle_heads=1,
+                margin_test=f"fwd+bwd walk B{B} H{H} S{S} D{D}")
 
 
 def test_large_sigma_stays_finite_and_accurate():

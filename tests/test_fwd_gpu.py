@@ -18,7 +18,9 @@ from attention.backward.fused_backward import _forward
 from attention.fused.fused import fused_attention
 from oracle import attention_oracle as orc
 from oracle import cases
-from tests.gpu_util import check_forward, dev, log
+from tests.gpu_util import check_forward, dev, log, margin
+
+LOG2E = 1.4426950408889634
 
 pytestmark = pytest.mark.gpu
 
@@ -86,7 +88,23 @@ def test_full_size_bf16_B4_H32_S4096_D128(tiles):
     log(f"full-size MHA bf16 {shape} tiles={tiles}")
     o = fused_attention(q, k, v, *tiles)
     torch.cuda.synchronize()
-    check_forward(o, q, k, v, rows_count=32, label=f"MHA {shape} {tiles}")
+    check_forward(o, q, k, v, rows_count=32, label=f"MHA {shape} {tiles}", tiles=tiles,
+                  margin_test="fwd B4 H32 S4096 D128")
+    # the forward that saves LSE (the training step's), every row against fp32 on the GPU
+    o2, lse = _forward(q, k, v, *tiles)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    S, D = shape[2], shape[3]
+    mask = torch.triu(torch.ones(S, S, device="cuda", dtype=torch.bool), 1)
+    err = 0.0
+    for b in range(shape[0]):
+        for h in range(shape[1]):
+            s = (q[b, h].float() @ k[b, h].float().t().contiguous()) / math.sqrt(D)
+            s.masked_fill_(mask, float("-inf"))
+            err = max(err, float((lse[b, h] - torch.logsumexp(s, -1) * LOG2E).abs().max()))
+    log(f"MHA {shape} {tiles} LSE max_abs={err:.3e} (bar {LSE_ABS['bf16']})")
+    margin("fwd+LSE B4 H32 S4096 D128", q, k, tiles, "LSE", err, LSE_ABS["bf16"])
+    assert err <= LSE_ABS["bf16"]
 
 
 # LSE bars: l sums P rounded to the input type, whose relative rounding error is at most

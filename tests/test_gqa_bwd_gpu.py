@@ -24,7 +24,7 @@ from attention.gqa.fused_gqa import fused_gqa_attention_autograd
 from oracle import attention_oracle as orc
 from oracle import cases
 from oracle.cpu_reference import reference_grads_gqa
-from tests.gpu_util import dev, log
+from tests.gpu_util import dev, log, margin
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +47,7 @@ def make(B, H, Hkv, N, D, dtype, seed):
     return [dev(x, dtype) for x in (q, k, v, do)]
 
 
-def check(q, k, v, do, tiles, label, oracle=False):
+def check(q, k, v, do, tiles, label, oracle=False, margin_test=None):
     got = run(fused_gqa_attention_autograd, q, k, v, do, tiles)
     for name, g, ref_t in zip(("O", "dQ", "dK", "dV"), got, (q, q, k, v)):
         assert g.dtype == q.dtype and g.shape == ref_t.shape, name
@@ -62,6 +62,8 @@ def check(q, k, v, do, tiles, label, oracle=False):
         # N = 1 the exact dQ and dK are zero (a single key: P = 1, dP = Delta)
         rel = float((g.float() - r).norm() / max(float(r.norm()), MAX_ABS * r.numel() ** 0.5))
         msg.append(f"{name}:abs={a:.2e},ratio={ratio:.2f},rel={rel:.1e}")
+        if margin_test is not None:
+            margin(margin_test, q, k, tiles, name, a, MAX_ABS, mixed=ratio, rel=rel)
         assert rel <= REL, (label, name, a, rel)
         if name in ("O", "dQ"):
             assert a <= MAX_ABS, (label, name, a)
@@ -119,7 +121,7 @@ def test_gqa_backward_equals_group_sum_of_mha(group):
 def test_gqa_backward_full_size_B2_H32_Hkv8_S4096_D128_bf16():
     q, k, v, do = make(2, 32, 8, 4096, 128, torch.bfloat16, seed=11)
     log("gqa-bwd full-size B2 H32 Hkv8 S4096 D128 bf16")
-    check(q, k, v, do, (128, 64), "gqa-bwd B2H32Hkv8 S4096 D128")
+    check(q, k, v, do, (128, 64), "gqa-bwd B2H32Hkv8 S4096 D128", margin_test="GQA fwd+bwd B2 H32 Hkv8 S4096 D128")
 
 
 def test_mqa_backward_full_size_B1_H32_Hkv1_S4096_D64_fp16():
@@ -128,7 +130,7 @@ def test_mqa_backward_full_size_B1_H32_Hkv1_S4096_D64_fp16():
     k = k * 0.5
     v = v * 0.5
     log("mqa-bwd full-size B1 H32 Hkv1 S4096 D64 fp16")
-    check(q, k, v, do, (128, 64), "mqa-bwd B1H32Hkv1 S4096 D64")
+    check(q, k, v, do, (128, 64), "mqa-bwd B1H32Hkv1 S4096 D64", margin_test="MQA fwd+bwd B1 H32 Hkv1 S4096 D64")
 
 
 def _bwd_through_abi(q, k, v, o, do, lse, ws_bytes):

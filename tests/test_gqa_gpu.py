@@ -41,7 +41,8 @@ def test_full_size_gqa_bf16_B2_H32_Hkv8_S8192_D128(tiles):
     log(f"full-size GQA tiles={tiles}")
     o = fused_gqa_attention(q, k, v, *tiles)
     torch.cuda.synchronize()
-    check_forward(o, q, k, v, rows_count=24, label=f"GQA B2H32Hkv8 S8192 {tiles}")
+    check_forward(o, q, k, v, rows_count=24, label=f"GQA B2H32Hkv8 S8192 {tiles}", tiles=tiles,
+                  margin_test="GQA fwd B2 H32 Hkv8 S8192 D128")
 
 
 @pytest.mark.parametrize("tiles", [(64, 64), (128, 128)], ids=lambda t: f"{t[0]}x{t[1]}")
@@ -52,7 +53,8 @@ def test_full_size_mqa_fp16_B1_H32_Hkv1_S16384_D64(tiles):
     log(f"full-size MQA tiles={tiles}")
     o = fused_gqa_attention(q, k, v, *tiles)
     torch.cuda.synchronize()
-    check_forward(o, q, k, v, rows_count=24, label=f"MQA S16384 {tiles}")
+    check_forward(o, q, k, v, rows_count=24, label=f"MQA S16384 {tiles}", tiles=tiles,
+                  margin_test="MQA fwd B1 H32 Hkv1 S16384 D64")
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
