@@ -297,18 +297,21 @@ def measure(args, impls, tiles):
     return out
 
 
+# timing columns of a results CSV and how each is read back; SDPA rows carry no tiles
+_ROW_FIELDS = (("D", int), ("N", int), ("B", int), ("H", int), ("impl", str), ("tile_m", str),
+               ("tile_n", str), ("median_ms", str), ("tflops", str), ("dtype", str), ("pct_peak", str))
+
+
 def import_rows(path):
-    rows = []
+    """Timing rows of a results CSV written by this tracker (rows without a time are skipped)."""
     with open(path) as f:
-        for r in csv.DictReader(f):
-            if not r.get("median_ms"):
-                continue
-            sdpa = r.get("impl") == "sdpa"
-            rows.append(dict(D=int(r["D"]), N=int(r["N"]), B=int(r["B"]), H=int(r["H"]), impl=r["impl"],
-                             tile_m="-" if sdpa else (r.get("tile_m") or "-"),
-                             tile_n="-" if sdpa else (r.get("tile_n") or "-"),
-                             median_ms=r["median_ms"], tflops=r["tflops"], dtype=r.get("dtype", ""),
-                             pct_peak=r.get("pct_peak", "")))
+        found = [r for r in csv.DictReader(f) if r.get("median_ms")]
+    rows = []
+    for r in found:
+        row = {name: conv(r.get(name) or ("-" if name.startswith("tile_") else "")) for name, conv in _ROW_FIELDS}
+        if row["impl"] == "sdpa":
+            row["tile_m"] = row["tile_n"] = "-"
+        rows.append(row)
     return rows
 
 
@@ -464,19 +467,20 @@ def key_of(r):
 
 
 def find_ref(history, gpu, run, which):
-    nums = sorted({int(r["run"]) for r in history if r["gpu"] == gpu and int(r["run"]) < run})
-    if not nums:
+    """Run number to compare `run` with on the same GPU: the latest earlier one ("prev") or the
+    earliest ("first"); None for the first run on that GPU."""
+    earlier = {int(r["run"]) for r in history if r["gpu"] == gpu and int(r["run"]) < run}
+    if not earlier:
         return None
-    return nums[-1] if which == "prev" else nums[0]
+    return max(earlier) if which == "prev" else min(earlier)
 
 
 def change(new_ms, old_ms):
     """Relative time change of a row against an earlier run's same row, in words."""
-    if old_ms is None or old_ms <= 0:
+    if not old_ms or old_ms <= 0:
         return "-"
-    saved = 1.0 - new_ms / old_ms
-    word = "faster" if saved >= 0 else "slower"
-    return f"{100.0 * abs(saved):.1f}% {word}"
+    ratio = new_ms / old_ms
+    return f"{100.0 * abs(1.0 - ratio):.1f}% {'faster' if ratio <= 1.0 else 'slower'}"
 
 
 def build_markdown(run, ts, env, note, rows, history, profile=None, reason="", change_txt="", diff=None):
