@@ -212,7 +212,7 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
   fa::BwdFn fn = bwd_table(dtype, D, dq_block_m(block_m, D), block_n);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H, S, D, scale_log2, sm_scale, hip_stream,
-                nullptr, nullptr, 1, nullptr};
+                nullptr, nullptr, 1, nullptr, false};
   return fn(a);
 }
 
@@ -249,7 +249,7 @@ int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
   float* wsk = nsplit > 1 ? reinterpret_cast<float*>(ws) : nullptr;
   float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
-                wsk, wsv, nsplit, rowb};
+                wsk, wsv, nsplit, rowb, false};
   return fn(a);
 }
 
@@ -315,7 +315,7 @@ int fa_bwd_gqa_exact(const void* q, const void* k, const void* v, const void* o,
   float* wsk = nsplit > 1 ? reinterpret_cast<float*>(ws + rowb_bytes(B, H, S)) : nullptr;
   float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
   fa::BwdArgs a{q, k, v, o, d_o, lse, dq, dk, dv, B, H, H_kv, S, D, scale_log2, sm_scale, hip_stream,
-                wsk, wsv, nsplit, rowb};
+                wsk, wsv, nsplit, rowb, rowb == nullptr};
   return fn(a);
 }
 

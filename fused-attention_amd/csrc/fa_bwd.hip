@@ -1600,6 +1600,51 @@ void dkdv_reduce_kernel(const float* __restrict__ Pk, const float* __restrict__ 
   }
 }
 
+// ===========================================================================
+// Per-row terms without dQ: -LSE/c and -Delta of every query row into Rb
+// ===========================================================================
+// What dq_kernel stores for dK/dV when it runs first, for the order that runs dK/dV
+// first (fa_bwd, or fa_bwd_gqa without a workspace): the same two lanes per row
+// (lane c, half hh of D), the same v_dot2c order over the half's 8-wide pieces and the
+// same sum of the halves, so the terms, and every gradient formed from them, equal
+// that path's bitwise.  HBM-bound: reads O and dO once (4 D bytes per row) and LSE,
+// writes 8 bytes per row.  One wave = 32 rows.
+template <typename E, int D>
+__global__ __launch_bounds__(256)
+void rowterms_kernel(const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO,
+                     const float* __restrict__ Lse, float* __restrict__ Rb, int BH, int S, float scale_log2) {
+  constexpr int KT = D / 16;
+  const int lane = threadIdx.x & 63, c = lane & 31, hh = lane >> 5;
+  const long long rows = (long long)BH * S;
+  const long long row = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 32 + c;
+  const long long r = row < rows ? row : rows - 1;   // lanes past the end compute a valid row, store nothing
+  const uint16_t* dr = dO + r * D + 8 * hh;
+  const uint16_t* orr = O + r * D + 8 * hh;
+  float part = 0.f;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const u32x4 d = gload16(dr + 16 * t);
+    const u32x4 o = gload16(orr + 16 * t);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) part = dot_pair<E>(d[w], o[w], part);
+  }
+  const float delta = halfwave_sum(part);
+  if (hh == 0 && row < rows) {
+    const float inv_c = 1.0f / scale_log2;
+    Rb[row] = -Lse[row] * inv_c;
+    Rb[rows + row] = -delta;
+  }
+}
+
+template <typename E, int D>
+static bool launch_rowterms(const BwdArgs& a, float* rb) {
+  const long long rows = (long long)a.B * a.H * a.S;
+  const int grid = (int)((rows + 127) / 128);
+  hipLaunchKernelGGL((rowterms_kernel<E, D>), dim3(grid), dim3(256), 0, (hipStream_t)a.stream,
+                     (const uint16_t*)a.o, (const uint16_t*)a.d_o, a.lse, rb, a.B * a.H, a.S, a.scale_log2);
+  return hipGetLastError() == hipSuccess;
+}
+
 // ---------------------------------------------------------------------------
 template <typename E, int D, int BMQ, int BNK>
 static bool launch_dkdv(const BwdArgs& a) {
@@ -1671,6 +1716,15 @@ static int launch_bwd(const BwdArgs& a) {
   if (a.rowb) {
     if (!launch_dq<E, D, BMQ, BNK>(a)) return FA_ERR_LAUNCH;
     return launch_dkdv<E, D, 64, 128>(a) ? FA_OK : FA_ERR_LAUNCH;
+  }
+  // dK/dV first: dQ's own output buffer holds the per-row terms until dQ, which runs
+  // last and forms its own, overwrites it (8 bytes per row in a 2 D-byte row).  With
+  // form_delta (the study entry's variant) dK/dV forms them in every key tile instead.
+  if (!a.form_delta && (reinterpret_cast<uintptr_t>(a.dq) & 15) == 0) {
+    BwdArgs t = a;
+    t.rowb = static_cast<float*>(a.dq);
+    if (!launch_rowterms<E, D>(t, t.rowb) || !launch_dkdv<E, D, 64, 128>(t)) return FA_ERR_LAUNCH;
+    return launch_dq<E, D, BMQ, BNK>(a) ? FA_OK : FA_ERR_LAUNCH;
   }
   if (!launch_dkdv<E, D, 64, 128>(a)) return FA_ERR_LAUNCH;
   return launch_dq<E, D, BMQ, BNK>(a) ? FA_OK : FA_ERR_LAUNCH;

@@ -41,8 +41,11 @@ struct BwdArgs {
   float* wsv;
   int nsplit;
   // [2, B*H, S] fp32: -LSE/c and -Delta of every query row, written by the dQ
-  // kernel (then launched first) for the dK/dV kernel; null: dK/dV forms them
+  // kernel (then launched first) for the dK/dV kernel; null: dK/dV runs first, with
+  // the terms written into dQ's own buffer by a row-terms pass (dQ overwrites them
+  // last), or, with form_delta, formed by the dK/dV kernel in every key tile
   float* rowb;
+  bool form_delta;
 };
 
 // keys per dK/dV workgroup (4 waves x 32 keys), for the split heuristics on the host

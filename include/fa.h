@@ -74,9 +74,13 @@ FA_API int fa_fwd(const void* q, const void* k, const void* v, void* o, float* l
 
 /*
  * Recompute backward of the causal forward: dQ, dK, dV from Q, K, V, O, dO and
- * the LSE written by fa_fwd.  Two atomic-free kernels run in order on the stream:
- * dK/dV (one workgroup per key tile) then dQ (one workgroup per query tile).
- * Delta = rowsum(dO * O) is computed inside both kernels; no workspace.
+ * the LSE written by fa_fwd.  Atomic-free kernels run in order on the stream: a
+ * row pass writes -LSE/c and -Delta (Delta = rowsum(dO * O)) of every query row
+ * into the start of dq's own buffer (8 bytes of each row's 2 D bytes), dK/dV (one
+ * workgroup per key tile) reads them, then dQ (one workgroup per query tile) forms
+ * its own and overwrites dq.  No workspace.  When dq is not 16-byte aligned the
+ * dK/dV kernel forms Delta from the O and dO tiles of every key tile instead (same
+ * results up to the fp32 summation order of Delta, slower).
  *
  * Replaces attention/backward/fused_backward.py:173-184 (_backward: the torch
  * Delta op at :175 and the two launches at :180-183).
@@ -116,7 +120,9 @@ FA_API int fa_bwd(const void* q, const void* k, const void* v, const void* o,
  *
  * No counterpart in the reference, whose backward is MHA-only (_check at
  * attention/backward/fused_backward.py:154 rejects K/V of another head count);
- * fa_bwd(...) equals fa_bwd_gqa(..., H_kv = H, ..., NULL, 0, stream).
+ * fa_bwd(...) equals fa_bwd_gqa(..., H_kv = H, ..., NULL, 0, stream).  Without a
+ * workspace (or with one too small for the per-row terms) the row pass of fa_bwd
+ * keeps them in dq's buffer, with the same results as when the workspace holds them.
  */
 FA_API int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
                const void* d_o, const float* lse, void* dq, void* dk, void* dv,
@@ -162,6 +168,8 @@ FA_API size_t fa_noalloc_scratch_bytes(void);
  * fa_bwd_gqa_exact: fa_bwd_gqa with the dQ kernel at dq_block_m x dq_block_n and the
  *   dK/dV key tiles split nsplit ways (1..64; > 1 needs a workspace of
  *   8*B*H*S (rounded up to 256) + 8*B*H_kv*nsplit*S*D bytes, else FA_ERR_WORKSPACE).
+ *   A NULL workspace (nsplit 1) runs the dK/dV kernel that forms Delta in every key
+ *   tile it meets, then dQ: the variant the row terms replace, kept for measurement.
  * The queries return what fa_fwd / fa_bwd_gqa choose for a shape (0: invalid).
  */
 FA_API int fa_fwd_exact(const void* q, const void* k, const void* v, void* o, float* lse,

@@ -13,7 +13,9 @@ Claims checked:
   entries' bitwise, and so do dK and dV at the same split;
 * a split changes only the fp32 summation order of dK and dV: every split matches the
   unsplit result to that order (a few bf16 / fp16 units) and the fp32 reference within the
-  suites' bars.
+  suites' bars;
+* without a workspace the exact entry runs the dK/dV kernel that forms Delta itself (no other
+  entry point reaches it): dQ unchanged, dK and dV within the same bars.
 """
 
 import ctypes
@@ -62,7 +64,7 @@ def rowb_bytes(B, H, S):
     return (8 * B * H * S + 255) // 256 * 256
 
 
-def bwd(lib, q, k, v, o, do, lse, bm, bn, nsplit=None):
+def bwd(lib, q, k, v, o, do, lse, bm, bn, nsplit=None, workspace=True):
     B, H, S, D = q.shape
     Hkv = k.shape[1]
     dq, dk, dv = (torch.full_like(t, float("nan")) for t in (q, k, v))
@@ -73,8 +75,8 @@ def bwd(lib, q, k, v, o, do, lse, bm, bn, nsplit=None):
         ws = torch.empty(n, dtype=torch.uint8, device="cuda")
         code = lib.fa_bwd_gqa(*args, ptr(ws), n, stream())
     else:
-        n = rowb_bytes(B, H, S) + (8 * B * Hkv * nsplit * S * D if nsplit > 1 else 0)
-        ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        n = rowb_bytes(B, H, S) + (8 * B * Hkv * nsplit * S * D if nsplit > 1 else 0) if workspace else 0
+        ws = torch.empty(n, dtype=torch.uint8, device="cuda") if workspace else None
         code = lib.fa_bwd_gqa_exact(*args, nsplit, ptr(ws), n, stream())
     assert code == _lib.FA_OK, _lib.strerror(code)
     torch.cuda.synchronize()
@@ -143,3 +145,14 @@ def test_backward_exact_shapes_and_splits(B, H, Hkv, S, D, dtype):
             err = (got_t.float().cpu() - ref).abs()
             assert bool((err <= 2e-2 + 2e-2 * ref.abs()).all()), f"split {nsplit} against the fp32 reference"
     assert float((dq.float().cpu() - rq).abs().max()) <= 2e-2
+    # no workspace: the dK/dV kernel forms each row's Delta from the O and dO tiles of every key
+    # tile it meets, in another fp32 order than the dQ kernel's (and, at D = 128, from dP
+    # rounded once more); dQ runs after it and is unchanged
+    dq, dk, dv = bwd(lib, q, k, v, o, do, lse, 64, 64, nsplit=1, workspace=False)
+    assert torch.equal(dq, want[0]), "dQ with the Delta-forming dK/dV"
+    dd = max(float((dk.float() - want[1].float()).abs().max()), float((dv.float() - want[2].float()).abs().max()))
+    log(f"bwd exact, no workspace B={B} H={H} H_kv={Hkv} S={S} D={D} {dtype}: vs unsplit {dd:.3g}")
+    assert dd <= 8 * 2.0 ** -7 * max(1.0, float(rk.abs().max()), float(rv.abs().max()))
+    for got_t, ref in ((dk, rk), (dv, rv)):
+        err = (got_t.float().cpu() - ref).abs()
+        assert bool((err <= 2e-2 + 2e-2 * ref.abs()).all()), "Delta-forming dK/dV against the fp32 reference"
