@@ -101,7 +101,16 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
+# The current stream's raw handle: torch's direct accessor when it has one (about 0.1 us
+# against 2 us for current_stream(), which builds a Stream object; a small call is bound
+# by host time), else the public route.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device):
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_raw_stream(index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
@@ -155,7 +164,8 @@ def bwd(q, k, v, o, do, lse, dq, dk, dv, tile_m, tile_n):
     _require_device(q, k, v, o, do, lse, dq, dk, dv)
     B, H, S, D = q.shape
     H_kv = k.shape[1]
-    # (the size depends on the device only through its CU count, the same on every MI355X)
+    # (the size depends on the device only through its CU count, the same on every MI355X;
+    # the query costs about 0.4 us, so it is not cached)
     nbytes = lib.fa_bwd_gqa_workspace_size(B, H, H_kv, S, D)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
     code = lib.fa_bwd_gqa(_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse),

@@ -15,9 +15,8 @@ Backward = two atomic-free kernels on the same stream:
                 recomputing P from the LSE; dV = P^T dO, dK = scale * dS^T Q, reading
                 the per-row terms instead of forming Delta in every key tile.
   with dS = P * (dP - Delta) and dP = dO V^T.  (The C entry fa_bwd keeps the
-  reference's order, dK/dV then dQ, with Delta formed in both kernels and no
-  workspace; the results differ in Delta's fp32 summation order and, at D = 128,
-  in dS, which the workspace path forms from P rounded to fp16.)
+  reference's order with no workspace: a row pass writes the same per-row terms
+  into dQ's buffer, dK/dV reads them, then dQ runs; the results are the same.)
 
 Shapes: q, k, v are (B, H, N, D) float16 or bfloat16, any N (a partial last tile
 is masked), tiles 64 or 128.

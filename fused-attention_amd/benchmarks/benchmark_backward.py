@@ -170,8 +170,10 @@ def main(argv=None):
                     rows.append(dict(base, status="skipped (bf16)"))
                     continue
                 try:
-                    if not settled:
-                        T.settle_clocks(lambda: impls["fused"](q, k, v))
+                    if not settled:  # clocks and the autograd path, forward and backward
+                        qs, ks, vs = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+                        T.settle_clocks(lambda: impls["fused"](qs, ks, vs).backward(do))
+                        del qs, ks, vs
                         settled = True
                     f_ms, b_ms, fb_ms, mem = measure(impls[name], q, k, v, do, a.warmup, a.reps)
                     tf = total / (fb_ms * 1e-3) / 1e12
