@@ -47,7 +47,7 @@ SIGNATURES = {
     "fa_fwd_heads_per_wg": (_I, [_I, _I, _I, _I, _I, _I]),
     "fa_fwd_rows_per_wg": (_I, [_I, _I, _I, _I]),
     "fa_bwd_dq_rows_per_wg": (_I, [_I, _I]),
-    "fa_bwd_dkdv_split": (_I, [_I, _I, _I, _I]),
+    "fa_bwd_dkdv_split": (_I, [_I, _I, _I, _I, _I]),
     "fa_bwd_gqa_workspace_size": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "fa_supported": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "fa_strerror": (ctypes.c_char_p, [_I]),

@@ -92,9 +92,24 @@ def variants(groups):
         for wl, splits in (((1, 32, 1, 16384, 64, "fp16"), (4, 8, 16, 32)),
                            ((1, 8, 1, 16384, 128, "bf16"), (4, 8, 16, 32)),
                            ((1, 32, 4, 8192, 128, "bf16"), (1, 2, 4, 8)),
-                           ((1, 8, 8, 4096, 128, "bf16"), (1, 2, 4))):
+                           ((1, 8, 8, 4096, 128, "bf16"), (1, 2, 4)),
+                           ((1, 16, 16, 8192, 128, "bf16"), (1, 2, 4)),
+                           ((2, 32, 32, 8192, 128, "bf16"), (1, 2))):
             for ns in splits:
                 out.append(("rules", "split {} B{} H{} Hkv{} S{} D{}".format(ns, *wl[:5]), wl, "bwd",
+                            dict(bm=64, bn=64, nsplit=ns), ""))
+    if "splits" in groups:  # the dK/dV split rule: both dK/dV kernels, several grid sizes
+        for wl, splits in (((1, 32, 1, 4096, 128, "bf16"), (4, 8, 16, 32)),
+                           ((1, 4, 4, 8192, 128, "bf16"), (1, 2, 4, 8)),
+                           ((1, 8, 8, 4096, 128, "bf16"), (1, 2, 4)),
+                           ((1, 32, 4, 8192, 128, "bf16"), (1, 2, 4)),
+                           ((1, 8, 1, 16384, 128, "bf16"), (4, 8, 16)),
+                           ((1, 32, 1, 4096, 64, "fp16"), (8, 16, 32, 64)),
+                           ((1, 16, 16, 4096, 64, "fp16"), (1, 2, 4)),
+                           ((2, 16, 16, 4096, 64, "fp16"), (1, 2, 4)),
+                           ((1, 32, 1, 16384, 64, "fp16"), (8, 16, 32))):
+            for ns in splits:
+                out.append(("splits", "split {} B{} H{} Hkv{} S{} D{}".format(ns, *wl[:5]), wl, "bwd",
                             dict(bm=64, bn=64, nsplit=ns), ""))
     return out
 

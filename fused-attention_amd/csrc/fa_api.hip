@@ -49,8 +49,8 @@ fa::BwdFn bwd_table(int dtype, int D, int bm, int bn) {
 // 128-key tiles a wave holds two 128-key score tiles in flight and needs more
 // than the 256 VGPRs of two waves per SIMD, so the workgroup stays at 4 waves.
 // Counters (profiles/tile_study_mha_gqa_bwd.md, GQA B=2 H=32 H_kv=8 S=8192 D=128):
-// one head of 64 rows 813 TFLOP/s, MFMA busy 43.0 %; two heads 1112 / 61.7 %; four
-// heads 1122 / 56.4 %.
+// one head of 64 rows 905 TFLOP/s, MFMA busy 48.7 %; two heads 1179 / 72.7 %; four
+// heads 1198 / 64.6 %.
 int heads_per_wg(int group, int block_m, int block_n) {
   int cap = (block_n == 128 ? 128 : 256) / block_m;  // waves / (block_m / 32)
   if (cap > kMaxGroupHeadsPerWg) cap = kMaxGroupHeadsPerWg;
@@ -82,10 +82,11 @@ using fa::kMaxDevices;
 // workgroups per CU, where the heavy-first order cannot balance the causal
 // triangle (B=2 H=8 H_kv=1 S=8192 fp16, tile 64x64: D=128 0.328 -> 0.288 ms,
 // D=32 0.175 -> 0.123 ms; at B=2 H=32 H_kv=8, 2048 workgroups, four stay 3 %
-// faster).  Two heads of 64 rows still hold two waves per SIMD.  With the heavy-first
-// order of today's kernel (profiles/tile_study_mha_gqa_bwd.md): B=1 H=16 H_kv=4 S=4096
-// D=128 two heads 737 TFLOP/s, four 619; B=2 H=8 H_kv=1 S=8192 D=32 559 vs 532, and
-// equal at D=64 and D=128.
+// faster).  Two heads of 64 rows still hold two waves per SIMD.  Re-measured on the
+// current kernel (profiles/tile_study_mha_gqa_bwd.md): B=1 H=16 H_kv=4 S=4096 D=128
+// (one workgroup per CU at four heads) two heads 869 TFLOP/s, four 711; B=2 H=8
+// H_kv=1 S=8192 (two per CU) two / four heads D=32 646 / 604, D=64 891 / 907, D=128
+// 1014 / 1098: mixed at two workgroups per CU, kept.
 int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
   int gh = heads_per_wg(group, block_m, block_n);
   if (gh == 4 && (long long)B * (H / 4) * ((S + block_m - 1) / block_m) < 4LL * cu_count()) gh = 2;
@@ -97,28 +98,40 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
 // on it (bitwise).  A single-head workgroup of 64 rows holds two waves, and with
 // its K and V tiles double-buffered in LDS it gets one wave per SIMD or less;
 // where that is measured slower, tile_m = 64 runs as 128-row workgroups.
-// Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows: tile_n = 64:
-// D=128 685 -> 970, D=64 582 -> 809, D=32 358 -> 552; tile_n = 128: D=128 350 -> 637
-// (D <= 64 about equal, so left).  dQ: D = 128 only (both tile_n).
-// Counters (profiles/tile_study_mha_gqa_bwd.md, B=4 H=32 S=4096 bf16): 64 rows x 64 keys at
-// D=128 run 707 TFLOP/s with MFMA busy 36.8 % (one wave per SIMD), 128 rows 907 / 54.8 %.
-// dQ: 64 -> 128 rows at D=128 849 -> 1121 TFLOP/s (MFMA busy 42.6 -> 59.2 %); at D=64 920 -> 968
-// with 64-key tiles and 683 -> 972 with 128-key tiles; at D=32 703 -> 717.
+// Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows
+// (profiles/tile_study_mha_gqa_bwd.md): tile_n = 64: D=128 828 -> 1087 (MFMA busy
+// 43.9 -> 64.8 %: a 64-row workgroup holds one wave per SIMD), D=64 681 -> 943, D=32
+// 443 -> 677; tile_n = 128: D=128 475 -> 761 (D <= 64 about equal, so left).  dQ, D >= 64:
+// 64 -> 128 rows at D=128 868 -> 1138 (MFMA busy 43.4 -> 61.1 %), at D=64 945 -> 979 with
+// 64-key tiles and 716 -> 1008 with 128-key tiles; at D=32 729 -> 772 (left literal).
 int fwd_block_m(int block_m, int block_n, int D, int gh) {
   return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
 }
 int dq_block_m(int block_m, int D) { return (block_m == 64 && D >= 64) ? 128 : block_m; }
 
-// Workgroups the dK/dV kernel should have for its heavy-first order to balance: two
-// rounds of one workgroup per CU up to S = 4096, and one round more per 4096 keys
-// beyond, since the heaviest key tile's pairs grow with S while the average does not
-// keep up (a split costs an fp32 partial write, read and reduction, so it is kept to
-// what load balance needs).  Measured (profiles/tile_study_mha_gqa_bwd.md, dK/dV +
-// reduction): MQA B=1 H=32 S=16384 D=64, split 4 / 8 / 16 / 32: 3158 / 2215 / 2087 /
-// 2128 us; B=1 H=8 H_kv=1 S=16384 D=128, 4 / 8 / 16: 1457 / 1088 / 1122; GQA B=1 H=32
-// H_kv=4 S=8192 D=128, 2 / 4 / 8: 1115 / 1103 / 1142; MHA B=1 H=8 S=4096 D=128, 1 / 2 /
-// 4: 114 / 95 / 120; the headline B=4 H=32 S=4096: 1 / 2: 1304 / 1708.
-int dkdv_target_workgroups(int S) { return 2 * cu_count() * std::max(1, (S + 4095) / 4096); }
+// Work items (key-tile chunks) the dK/dV kernel should have for its heavy-first order
+// to balance: two per workgroup slot the GPU holds at once, and one round more per
+// 8192 keys beyond, since the heaviest key tile's pairs grow with S while the average
+// does not keep up (a split costs an fp32 partial write, read and reduction, so it is
+// kept to what load balance needs).  Slots: the paired D = 128 kernel runs one
+// persistent workgroup per CU that walks its items; the one-wave kernel (D <= 64) two
+// workgroups per CU, one per item.  Measured (profiles/dkdv_split_study.md, dK/dV +
+// reduction, us, the rule's choice first):
+//   paired: MQA B=1 H=32 S=4096 D=128, 16 / 8 / 32: 261 / 401 / 294; MHA B=1 H=4 S=8192,
+//   2 / 1 / 4: 143 / 202 / 161; MHA B=1 H=8 S=4096, 2 / 1 / 4: 86 / 98 / 106; GQA B=1 H=32
+//   H_kv=4 S=8192, 2 / 1 / 4: 977 / 1542 / 1000; B=1 H=8 H_kv=1 S=16384, 8 / 4 / 16: 972 /
+//   1264 / 1022;
+//   one-wave: MQA B=1 H=32 S=4096 D=64, 32 / 16 / 64: 181 / 211 / 191; MHA B=1 H=16 S=4096
+//   D=64, 2 / 1 / 4: 97 / 107 / 113; B=2 H=16 S=4096 D=64, 1 / 2: 155 / 188; MQA B=1 H=32
+//   S=16384 D=64, 16 / 8 / 32: 2017 / 2140 / 2053.
+// (The previous rule, 2 x CU items per 4096 keys for both kernels, chose 4 for MHA
+// B=1 H=4 S=8192 and for the GQA shape, 16 for B=1 H=8 H_kv=1 and for MQA S=4096 D=64, and
+// 1 for MHA B=1 H=16 D=64: 13, 2, 5, 16 and 10 % slower.)  D = 32 runs the one-wave kernel
+// and takes its rule unmeasured.
+int dkdv_target_workgroups(int S, int D) {
+  const int slots = cu_count() * (D == 128 ? 1 : 2);
+  return 2 * slots * std::max(1, (S + 8191) / 8192);
+}
 
 size_t gqa_workspace_bytes(int B, int H_kv, int S, int D, int nsplit) {
   return nsplit > 1 ? 2 * (size_t)B * H_kv * nsplit * S * D * sizeof(float) : 0;
@@ -131,17 +144,18 @@ size_t rowb_bytes(int B, int H, int S) {
 }
 
 // Chunks per key tile for dK/dV: enough that B * H_kv * (key tiles) * nsplit
-// reaches the target number of workgroups, at most the pairs of the heaviest key
+// reaches the target number of work items, at most the pairs of the heaviest key
 // tile (G query heads x all 64-row query tiles) and kMaxDkdvSplit; 1 when the key
-// tiles alone already fill the GPU, or when the heaviest tile has fewer than
+// tiles alone already reach it, or when the heaviest tile has fewer than
 // kMinSplitPairs pairs: then the partial-sum traffic and the extra pass cost more
-// than the imbalance (measured: B=2 H=8 S=2048 D=128 0.133 ms whole, 0.146 ms split;
-// B=1 H=8 S=4096 0.241 -> 0.217 ms; MQA H=32 S=4096 3.17 -> 0.42 ms).
+// than the imbalance (profiles/tile_study_mha_gqa_bwd.md, dK/dV + reduction: B=2 H=8
+// S=2048 D=128, 32 pairs, 57 us whole against 282 at split 16; B=1 H=8 S=4096, 64
+// pairs, 98 -> 86 us at split 2; MQA B=1 H=32 S=4096 D=64 1748 -> 196 us at split 64).
 constexpr int kMaxDkdvSplit = 64;
 constexpr int kMinSplitPairs = 64;
-int dkdv_nsplit(int B, int H, int H_kv, int S) {
+int dkdv_nsplit(int B, int H, int H_kv, int S, int D) {
   const long long items = (long long)B * H_kv * ((S + fa::kDkdvKeys - 1) / fa::kDkdvKeys);
-  const long long want = dkdv_target_workgroups(S);
+  const long long want = dkdv_target_workgroups(S, D);
   const long long pairs = (long long)(H / H_kv) * ((S + 63) / 64);
   if (items >= want || pairs < kMinSplitPairs) return 1;
   long long s = (want + items - 1) / items;
@@ -219,7 +233,7 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* o,
 size_t fa_bwd_gqa_workspace_size(int B, int H, int H_kv, int S, int D) {
   if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
   if (D != 32 && D != 64 && D != 128) return 0;
-  return rowb_bytes(B, H, S) + gqa_workspace_bytes(B, H_kv, S, D, dkdv_nsplit(B, H, H_kv, S));
+  return rowb_bytes(B, H, S) + gqa_workspace_bytes(B, H_kv, S, D, dkdv_nsplit(B, H, H_kv, S, D));
 }
 
 int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
@@ -244,7 +258,7 @@ int fa_bwd_gqa(const void* q, const void* k, const void* v, const void* o,
     ws += rowb_bytes(B, H, S);
     left -= rowb_bytes(B, H, S);
   }
-  int nsplit = workspace ? dkdv_nsplit(B, H, H_kv, S) : 1;
+  int nsplit = workspace ? dkdv_nsplit(B, H, H_kv, S, D) : 1;
   while (nsplit > 1 && gqa_workspace_bytes(B, H_kv, S, D, nsplit) > left) --nsplit;
   float* wsk = nsplit > 1 ? reinterpret_cast<float*>(ws) : nullptr;
   float* wsv = nsplit > 1 ? wsk + (size_t)B * H_kv * nsplit * S * D : nullptr;
@@ -332,9 +346,10 @@ int fa_fwd_rows_per_wg(int block_m, int block_n, int D, int heads_per_wg) {
 
 int fa_bwd_dq_rows_per_wg(int block_m, int D) { return tile_ok(block_m) ? dq_block_m(block_m, D) : 0; }
 
-int fa_bwd_dkdv_split(int B, int H, int H_kv, int S) {
+int fa_bwd_dkdv_split(int B, int H, int H_kv, int S, int D) {
   if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
-  return dkdv_nsplit(B, H, H_kv, S);
+  if (D != 32 && D != 64 && D != 128) return 0;
+  return dkdv_nsplit(B, H, H_kv, S, D);
 }
 
 int fa_supported(int dtype, int D, int block_m, int block_n, int group, int with_lse, int is_bwd) {

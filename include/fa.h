@@ -183,7 +183,7 @@ FA_API int fa_bwd_gqa_exact(const void* q, const void* k, const void* v, const v
 FA_API int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int block_m, int block_n);
 FA_API int fa_fwd_rows_per_wg(int block_m, int block_n, int D, int heads_per_wg);
 FA_API int fa_bwd_dq_rows_per_wg(int block_m, int D);
-FA_API int fa_bwd_dkdv_split(int B, int H, int H_kv, int S);
+FA_API int fa_bwd_dkdv_split(int B, int H, int H_kv, int S, int D);
 
 /* Workspace bytes fa_bwd_gqa uses for this shape on the current device: the
  * per-row terms, plus the partial sums when the key tiles alone leave the GPU

@@ -122,16 +122,19 @@ def rowb(B, H, S):
 
 def test_bwd_gqa_workspace_size(lib):
     """The per-row terms, then fp32 partial dK and dV per chunk: 2 * B * H_kv * nsplit * S * D * 4
-    bytes, with nsplit the chunks per 128-key tile that give 2 x 256 dK/dV workgroups (times
-    ceil(S / 4096)), at most the
-    heaviest key tile's (query tile, query head) pairs and 64 (no split below 64 pairs)."""
+    bytes, with nsplit the chunks per 128-key tile that give two work items per dK/dV workgroup
+    slot (the paired D = 128 kernel: one per CU, 256; the one-wave kernel at D <= 64: two per CU)
+    times ceil(S / 8192), at most the heaviest key tile's (query tile, query head) pairs and 64
+    (no split below 64 pairs)."""
     ws = lib.fa_bwd_gqa_workspace_size
     assert ws(2, 32, 32, 4096, 128) == rowb(2, 32, 4096)              # 2*32*32 key tiles: no split
-    assert ws(2, 32, 8, 4096, 128) == rowb(2, 32, 4096)               # 2*8*32 = 512 workgroups already
+    assert ws(2, 32, 8, 4096, 128) == rowb(2, 32, 4096)               # 2*8*32 = 512 items already
     assert ws(1, 8, 8, 4096, 128) == rowb(1, 8, 4096) + 2 * 8 * 2 * 4096 * 128 * 4  # MHA, 256 key tiles: 2 chunks
-    assert ws(1, 32, 1, 4096, 64) == rowb(1, 32, 4096) + 2 * 16 * 4096 * 64 * 4   # MQA: 32 key tiles x 16 chunks
-    # S = 8192: target 2 x 2 x 256 workgroups, 4 x 64 key tiles -> 4 chunks
-    assert ws(1, 32, 4, 8192, 128) == rowb(1, 32, 8192) + 2 * 4 * 4 * 8192 * 128 * 4
+    assert ws(1, 32, 1, 4096, 64) == rowb(1, 32, 4096) + 2 * 32 * 4096 * 64 * 4   # MQA: 32 key tiles x 32 chunks
+    # S = 8192, D = 128: target 512, 4 x 64 key tiles -> 2 chunks
+    assert ws(1, 32, 4, 8192, 128) == rowb(1, 32, 8192) + 2 * 4 * 2 * 8192 * 128 * 4
+    # S = 16384: target 2 x 512 (D = 128), 8 x 128 key tiles -> 8 chunks
+    assert ws(1, 8, 1, 16384, 128) == rowb(1, 8, 16384) + 2 * 8 * 16384 * 128 * 4
     assert ws(1, 6, 2, 100, 32) == rowb(1, 6, 100)                    # 3 heads x 2 query tiles: too short to split
     assert ws(1, 32, 1, 200, 32) == rowb(1, 32, 200) + 2 * 64 * 200 * 32 * 4  # 2 key tiles of 32 x 4 pairs: 64 chunks (the cap)
     assert ws(2, 8, 8, 2048, 128) == rowb(2, 8, 2048)                 # 32 pairs per key tile: not worth a split
@@ -228,8 +231,17 @@ def test_exact_shape_entries_and_rule_queries(lib):
     assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 64) == 2
     assert lib.fa_fwd_heads_per_wg(2, 8, 1, 1024, 64, 64) == 2     # 4 -> 2: under 4 workgroups per CU
     assert lib.fa_fwd_heads_per_wg(1, 32, 1, 16384, 64, 128) == 2
-    assert lib.fa_bwd_dkdv_split(4, 32, 32, 4096) == 1
-    assert lib.fa_bwd_dkdv_split(1, 32, 1, 4096) == 16   # 32 key tiles, target 512 workgroups
-    assert lib.fa_bwd_dkdv_split(1, 32, 1, 16384) == 16  # 128 key tiles, target 4 x 512
-    assert lib.fa_bwd_dkdv_split(1, 8, 8, 4096) == 2
-    assert lib.fa_fwd_heads_per_wg(0, 32, 8, 4096, 64, 64) == 0 and lib.fa_bwd_dkdv_split(1, 4, 3, 64) == 0
+    # dK/dV split: two items per workgroup slot (the paired D = 128 kernel one slot per CU, the
+    # one-wave kernel two), one round more per 8192 keys; no split under 64 pairs per key tile
+    assert lib.fa_bwd_dkdv_split(4, 32, 32, 4096, 128) == 1
+    assert lib.fa_bwd_dkdv_split(1, 32, 1, 4096, 128) == 16    # 32 key tiles, target 512
+    assert lib.fa_bwd_dkdv_split(1, 32, 1, 4096, 64) == 32     # target 1024
+    assert lib.fa_bwd_dkdv_split(1, 32, 1, 16384, 64) == 16    # 128 key tiles, target 2 x 1024
+    assert lib.fa_bwd_dkdv_split(1, 8, 1, 16384, 128) == 8     # target 2 x 512
+    assert lib.fa_bwd_dkdv_split(1, 8, 8, 4096, 128) == 2
+    assert lib.fa_bwd_dkdv_split(1, 4, 4, 8192, 128) == 2      # 256 key tiles, target 512
+    assert lib.fa_bwd_dkdv_split(1, 16, 16, 4096, 64) == 2     # 512 key tiles, target 1024
+    assert lib.fa_bwd_dkdv_split(2, 16, 16, 4096, 64) == 1
+    assert lib.fa_bwd_dkdv_split(2, 8, 8, 2048, 128) == 1      # 32 pairs per key tile
+    assert lib.fa_fwd_heads_per_wg(0, 32, 8, 4096, 64, 64) == 0 and lib.fa_bwd_dkdv_split(1, 4, 3, 64, 128) == 0
+    assert lib.fa_bwd_dkdv_split(1, 4, 4, 64, 48) == 0

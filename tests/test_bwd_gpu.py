@@ -132,7 +132,7 @@ def test_long_sequence_bf16_D128_takes_the_alternating_walk(shape):
     B, H, S, D = shape
     lib = _lib.load()
     assert S * D * 4 >= 4 << 20  # the walk's rule: G * S * D * 4 bytes of Q and dO per K/V head
-    split = lib.fa_bwd_dkdv_split(B, H, H, S)
+    split = lib.fa_bwd_dkdv_split(B, H, H, S, D)
     q, k, v, do = inputs(shape, seed=S + H, dtype=torch.bfloat16)
     log(f"bwd walk MHA bf16 {shape} (dK/dV split {split})")
     check_grads(q, k, v, do, (64, 64), f"bwd walk {shape} split {split}", oracle_heads=1,
@@ -225,7 +225,7 @@ def test_reference_entry_without_workspace(shape, dt, tiles):
     q, k, v, do = inputs(shape, seed=sum(shape), dtype=DTYPES[dt])
     log(f"fa_bwd without workspace {shape} {dt} {tiles}")
     B, H, S, D = shape
-    assert _lib.load().fa_bwd_dkdv_split(B, H, H, S) == 1
+    assert _lib.load().fa_bwd_dkdv_split(B, H, H, S, D) == 1
     got = _fa_bwd_no_workspace(q, k, v, do, tiles)
     py = run_fused(q, k, v, do, tiles)[1:]
     for name, g, p in zip(("dQ", "dK", "dV"), got, py):

@@ -121,7 +121,7 @@ def test_backward_exact_shapes_and_splits(B, H, Hkv, S, D, dtype):
     lib = _lib.load()
     q, k, v, do = inputs(B, H, Hkv, S, D, dtype, seed=3 * S + D)
     o, lse = fwd(lib, q, k, v, 64, 64)
-    base_split = lib.fa_bwd_dkdv_split(B, H, Hkv, S)
+    base_split = lib.fa_bwd_dkdv_split(B, H, Hkv, S, D)
     want = bwd(lib, q, k, v, o, do, lse, 64, 64)
     # dQ rows per workgroup: the exact 64-row dQ against the dispatch's (128 rows at D >= 64)
     got = bwd(lib, q, k, v, o, do, lse, 64, 64, nsplit=base_split)

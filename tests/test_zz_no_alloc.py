@@ -66,7 +66,7 @@ def test_noalloc_backward_equals_workspace_backward_on_consecutive_calls():
     assert cap == 64 << 20
     ws = torch.empty(cap, dtype=torch.uint8, device="cuda")  # the caller workspace of the same size
     for i, (B, H, Hkv, S, D, dtype, tiles) in enumerate(CALLS):
-        split = lib.fa_bwd_dkdv_split(B, H, Hkv, S)
+        split = lib.fa_bwd_dkdv_split(B, H, Hkv, S, D)
         need = lib.fa_bwd_gqa_workspace_size(B, H, Hkv, S, D)
         log(f"noalloc call {i}: B={B} H={H} H_kv={Hkv} S={S} D={D} {dtype} tiles={tiles} split={split} "
             f"full workspace {need} bytes ({'fits' if need <= cap else 'exceeds'} the {cap}-byte scratch)")
