@@ -1054,8 +1054,10 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   auto rd_sd = [&](const unsigned char* buf, int j) __attribute__((always_inline)) {
     return lds_read16(buf + a1, to.opnd[j >> 1] + 32 * (j & 1) * ROWB);
   };
+  // S / dP and dV / dK MFMAs per wave and pair: 2 KT and 4 DB (16 and 16 at D = 128)
+  constexpr int NS = 2 * KT, NV = 4 * DB, NT = NS + NV;
   auto rd_w = [&](const unsigned char* buf, int j) __attribute__((always_inline)) {
-    const int qb = j >> 3, db = (j >> 1) & 3, i1 = j & 1;
+    const int qb = j / (2 * DB), db = (j >> 1) % DB, i1 = j & 1;
     return tr_read2(buf + a2, to.tr(db, 2 * qb + i1, 0), to.tr(db, 2 * qb + i1, 1));
   };
   // A stream also issues pair t+2's DMA.  The source places one part every other
@@ -1075,7 +1077,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     const unsigned char* bc = bufp(t);
     x[0] = load_rows(reinterpret_cast<const float*>(bn + lo), 0);
     x[1] = load_rows(reinterpret_cast<const float*>(bn + lo), 1);
-    auto rd = [&](int i) __attribute__((always_inline)) { return i < 16 ? rd_sd(bn, i) : rd_w(bc, i - 16); };
+    auto rd = [&](int i) __attribute__((always_inline)) { return i < NS ? rd_sd(bn, i) : rd_w(bc, i - NS); };
     u32x4 hp[2][2];  // fp16 copy of P for the slot (bf16 input)
     // P of query block qb, elements 4k .. 4k+3 (k = 0..3)
     auto p_chunk = [&](int qb, int k) __attribute__((always_inline)) {
@@ -1095,20 +1097,23 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     u32x4 rot[PD + 1];
 #pragma unroll
     for (int i = 0; i < PD; ++i) rot[i] = rd(i);
-    static_for<0, 32>([&](auto I) __attribute__((always_inline)) {
+    // S of block 0 is complete after MFMA NS - 2, of block 1 after NS - 1; P's four
+    // chunks of a block go out every SP-th dV MFMA from C0 (block 0) and C1 (block 1)
+    // (D = 128: 17, 19, 21, 23 and 25 .. 31)
+    constexpr int SP = NV / 8, C0 = NS + SP - 1, C1 = C0 + NV / 2;
+    static_for<0, NT>([&](auto I) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
-      if constexpr (i + PD < 32) rot[(i + PD) % (PD + 1)] = rd(i + PD);
+      if constexpr (i + PD < NT) rot[(i + PD) % (PD + 1)] = rd(i + PD);
       if constexpr (i % 2 == 0 && i / 2 <= 2 * NDMA)
         if (dm) dma_part(job, i / 2);
-      if constexpr (i < 16) {
+      if constexpr (i < NS) {
         x[i & 1] = mfma32<E>(rot[i % (PD + 1)], xf[i >> 1], x[i & 1]);
       } else {
-        constexpr int j = i - 16, qb = j >> 3, db = (j >> 1) & 3, i1 = j & 1;
+        constexpr int j = i - NS, qb = j / (2 * DB), db = (j >> 1) % DB, i1 = j & 1;
         acc[db] = mfma32<E>(rot[i % (PD + 1)], pcur[qb][i1], acc[db]);
       }
-      // S of block 0 is complete after MFMA 14, of block 1 after 15
-      if constexpr (i >= 17 && i <= 23 && (i - 17) % 2 == 0) p_chunk(0, (i - 17) / 2);
-      if constexpr (i >= 25 && (i - 25) % 2 == 0) p_chunk(1, (i - 25) / 2);
+      if constexpr (i >= C0 && i < C0 + 4 * SP && (i - C0) % SP == 0) p_chunk(0, (i - C0) / SP);
+      if constexpr (i >= C1 && i < C1 + 4 * SP && (i - C1) % SP == 0) p_chunk(1, (i - C1) / SP);
       __builtin_amdgcn_sched_barrier(0);
     });
   };
@@ -1124,7 +1129,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int i1 = 0; i1 < 2; ++i1) w[qb][i1] = *slot(t, qb, i1);
-    auto rd = [&](int i) __attribute__((always_inline)) { return i < 16 ? rd_w(bc, i) : rd_sd(bn, i - 16); };
+    auto rd = [&](int i) __attribute__((always_inline)) { return i < NV ? rd_w(bc, i) : rd_sd(bn, i - NV); };
     // dS of query block qb, elements 4k .. 4k+3
     auto ds_chunk = [&](int qb, int k) __attribute__((always_inline)) {
       const int i1 = k >> 1, q0 = 2 * (k & 1);
@@ -1139,24 +1144,30 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     u32x4 rot[PD + 1];
 #pragma unroll
     for (int i = 0; i < PD; ++i) rot[i] = rd(i);
+    // block 1's dS under block 0's dK MFMAs when there are 8 of them (D = 128); with
+    // fewer, all of dS first
+    constexpr bool DS1_IN = NV >= 16;
 #pragma unroll
     for (int k = 0; k < 4; ++k) ds_chunk(0, k);
+    if constexpr (!DS1_IN)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ds_chunk(1, k);
     __builtin_amdgcn_sched_barrier(0);
-    static_for<0, 32>([&](auto I) __attribute__((always_inline)) {
+    static_for<0, NT>([&](auto I) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
-      if constexpr (i + PD < 32) rot[(i + PD) % (PD + 1)] = rd(i + PD);
+      if constexpr (i + PD < NT) rot[(i + PD) % (PD + 1)] = rd(i + PD);
       if constexpr (i % 2 == 0 && i / 2 <= 2 * NDMA)
         if (dm) dma_part(job, i / 2);
-      if constexpr (i < 4) ds_chunk(1, i);
-      if constexpr (i == 8) {  // dS is formed: x takes dP(t+1) - Delta
+      if constexpr (DS1_IN && i < 4) ds_chunk(1, i);
+      if constexpr (i == NV / 2) {  // dS is formed: x takes dP(t+1) - Delta
         x[0] = load_rows(reinterpret_cast<const float*>(bn + lo), 0);
         x[1] = load_rows(reinterpret_cast<const float*>(bn + lo), 1);
       }
-      if constexpr (i < 16) {
-        constexpr int qb = i >> 3, db = (i >> 1) & 3, i1 = i & 1;
+      if constexpr (i < NV) {
+        constexpr int qb = i / (2 * DB), db = (i >> 1) % DB, i1 = i & 1;
         acc[db] = mfma32<E>(rot[i % (PD + 1)], bop[qb][i1], acc[db]);
       } else {
-        constexpr int j = i - 16;
+        constexpr int j = i - NV;
         x[j & 1] = mfma32<E>(rot[i % (PD + 1)], xf[j >> 1], x[j & 1]);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1652,6 +1663,9 @@ static bool launch_dkdv(const BwdArgs& a) {
   const int nsplit = a.nsplit > 1 ? a.nsplit : 1;
   const dim3 grid(a.B * a.Hkv * nsplit * ((a.S + BNK - 1) / BNK)), block(2 * BNK);
   bool paired = false;
+  // (the paired kernel's streams are written for any D; at D = 64 it measured slower
+  // than the one-wave kernel, which already holds two waves per SIMD there: backward
+  // -6.0 % at B=2 H=16 S=4096 fp16, -3.5 % MQA B=1 H=32 S=4096, -12.6 % B=4 H=32 bf16)
   if constexpr (FA_DKDV_PAIR && D == 128) {
     if (a.rowb) {
       // one workgroup per CU walks the key tiles (the kernel reads the grid size); the
