@@ -82,6 +82,33 @@ def load():
     return lib
 
 
+_autograd = None
+
+
+def autograd():
+    """The C++ autograd op (fa_autograd, built by csrc/build_autograd.py next to libfa.so);
+    raise LibraryError (never fall back) if it is absent."""
+    global _autograd
+    if _autograd is not None:
+        return _autograd
+    load()  # the op calls into libfa.so; load (and check) it first
+    import importlib.util
+    import sysconfig
+    path = os.path.join(_PKG_ROOT, "fa_autograd" + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not os.path.exists(path):
+        raise LibraryError(
+            f"{path} not found; build it with `python3 fused-attention_amd/csrc/build_autograd.py` "
+            f"(or __graft_entry__.build()) before using the fused autograd entry points")
+    spec = importlib.util.spec_from_file_location("fa_autograd", path)
+    try:
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+    except ImportError as e:
+        raise LibraryError(f"could not load {path}: {e}") from e
+    _autograd = mod
+    return mod
+
+
 def strerror(code):
     return load().fa_strerror(code).decode()
 

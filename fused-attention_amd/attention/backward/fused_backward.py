@@ -71,5 +71,11 @@ class FusedAttentionFn(torch.autograd.Function):
 
 
 def fused_attention_autograd(q, k, v, tile_m=64, tile_n=64):
-    """Causal attention (B, H, N, D) float16/bfloat16 with autograd support."""
-    return FusedAttentionFn.apply(q, k, v, tile_m, tile_n)
+    """Causal attention (B, H, N, D) float16/bfloat16 with autograd support.
+
+    The checks of FusedAttentionFn, then the same forward and backward as a C++ autograd node
+    (csrc/fa_autograd.cpp): results bitwise equal to FusedAttentionFn.apply, without Python in
+    the backward (the host path is what bounds short sequences)."""
+    _check(q, k, v, tile_m, tile_n)
+    _lib._require_device(q, k, v)
+    return _lib.autograd().fused_attention(q, k, v, int(tile_m), int(tile_n))

@@ -70,5 +70,14 @@ class FusedGQAAttentionFn(torch.autograd.Function):
 
 
 def fused_gqa_attention_autograd(q, k, v, tile_m=64, tile_n=64):
-    """Causal GQA/MQA attention, q (B, H, N, D), k/v (B, H_kv, N, D), with autograd."""
-    return FusedGQAAttentionFn.apply(q, k, v, tile_m, tile_n)
+    """Causal GQA/MQA attention, q (B, H, N, D), k/v (B, H_kv, N, D), with autograd.
+
+    The checks of FusedGQAAttentionFn, then the same forward and backward as a C++ autograd
+    node (csrc/fa_autograd.cpp), bitwise equal to FusedGQAAttentionFn.apply."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, H, N, D); got {tuple(q.shape)}")
+    _check_gqa(q, k, v, tile_m, tile_n)
+    if q.dtype not in _DTYPES:
+        raise TypeError("q, k, v must all be float16 or all be bfloat16")
+    _lib._require_device(q, k, v)
+    return _lib.autograd().fused_attention(q, k, v, int(tile_m), int(tile_n))

@@ -154,3 +154,12 @@ def test_unfused_backends_match_oracle_on_cpu():
     # the eager baseline has no tiles: any N, like the fused backends (here N = 64, tile 48)
     np.testing.assert_allclose(unfused_attention(q, q, q, 48, 64).numpy(),
                                orc.forward(q.numpy(), q.numpy(), q.numpy()), atol=2e-5)
+
+
+def test_autograd_node_loads_without_a_gpu():
+    """The C++ autograd node (fa_autograd, over libfa.so) is built in-tree and imports on a host
+    without a GPU; the Python wrappers check their arguments before reaching it."""
+    from attention import _lib
+    mod = _lib.autograd()
+    assert callable(mod.fused_attention)
+    assert _lib.autograd() is mod
