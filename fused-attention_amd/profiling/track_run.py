@@ -178,14 +178,13 @@ def load_fused(kernel_path):
     if kernel_path in (None, "", DEFAULT_KERNEL):
         from attention.fused.fused import fused_attention
         return fused_attention
-    import importlib.util
+    import runpy
     path = os.path.abspath(kernel_path if os.path.exists(kernel_path) else os.path.join(PKG_ROOT, kernel_path))
-    name = "tracked_" + re.sub(r"\W", "_", os.path.splitext(os.path.basename(path))[0])
-    spec = importlib.util.spec_from_file_location(name, path)
-    mod = importlib.util.module_from_spec(spec)
-    sys.modules[name] = mod
-    spec.loader.exec_module(mod)
-    return mod.fused_attention
+    # the file's top level runs once, as a script would; its fused_attention is the entry
+    namespace = runpy.run_path(path, run_name="tracked_" + re.sub(r"\W", "_", os.path.basename(path)))
+    if "fused_attention" not in namespace:
+        raise AttributeError(f"{kernel_path} defines no fused_attention")
+    return namespace["fused_attention"]
 
 
 def torch_dtype(name):
