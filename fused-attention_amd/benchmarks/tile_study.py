@@ -358,7 +358,7 @@ def report(rows, commands):
 
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    p.add_argument("--out-dir", default=os.path.join(os.path.dirname(PKG_ROOT), "gpurun_out", "tile_study"))
+    p.add_argument("--out-dir", default=os.path.join(os.path.dirname(PKG_ROOT), "out", "tile_study"))
     p.add_argument("--groups", default="fwd,gqa,dq,dkdv")
     p.add_argument("--rounds", type=int, default=3,
                    help="passes over all variants in the timing pass (interleaves them in time)")

@@ -40,10 +40,10 @@ def lib():
 
 def pytest_sessionfinish(session, exitstatus):
     """Write the per-case records of the reference suites (tests/gpu_util.RECORDS) as CSVs in
-    the reference's layout under $FA_RECORDS_DIR (default gpurun_out/correctness/)."""
+    the reference's layout under $FA_RECORDS_DIR (default out/correctness/ at the repository root)."""
     mod = sys.modules.get("tests.gpu_util") or sys.modules.get("gpu_util")
     if mod is None or not getattr(mod, "RECORDS", None):
         return
-    root = os.environ.get("FA_RECORDS_DIR", os.path.join(REPO_ROOT, "gpurun_out", "correctness"))
+    root = os.environ.get("FA_RECORDS_DIR", os.path.join(REPO_ROOT, "out", "correctness"))
     for path in mod.write_records(root):
         print(f"\nper-case record: {os.path.relpath(path, REPO_ROOT)}")
