@@ -666,7 +666,12 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   constexpr int OFF_L = 2 * TILE;                        // Q | dO | -LSE/c | -Delta
   constexpr int BUFA = (OFF_L + 2 * BMQ * 4 + 1023) / 1024 * 1024;
   constexpr int NBUF = 3;
-  constexpr int NDMA = (NBLK + NW - 1) / NW;
+  // DMA waves: all eight, or with WALK the four of role 0 (role 1's stream is the longer
+  // one, and on the alternating walk the role-0 DMA measured +1.6 % and +2.2 % at GQA
+  // B=2 H=32 H_kv=8 S=4096 and B=1 H=32 H_kv=4 S=8192; on the upward walk -1.2 % at
+  // B=4 H=32 S=4096)
+  constexpr int NDW = WALK ? NW / 2 : NW;
+  constexpr int NDMA = NBLK / NDW;
   constexpr int XPS = NKB * 2 * 2 * 64;                  // 16-byte P pieces per slot
   static_assert(TILE % 1024 == 0 && NBLK % NW == 0, "tiles are whole 1 KB DMA blocks, split evenly");
   const float NEG_INF = -__builtin_inff();
@@ -780,13 +785,13 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     }
   };
 
-  // DMA of pair (di, dg)'s Q and dO tiles and its two row-term slices: every wave
+  // DMA of pair (di, dg)'s Q and dO tiles and its two row-term slices: each DMA wave
   // copies NDMA 1 KB blocks of each tile, waves 0 and 1 one slice each
   const int drow = lane / CPR, dch = lane % CPR;
   int dvo[NDMA];
 #pragma unroll
   for (int x = 0; x < NDMA; ++x) {
-    const int row = (wave + x * NW) * (1024 / ROWB) + drow;
+    const int row = (wave % NDW + x * NDW) * (1024 / ROWB) + drow;
     dvo[x] = row * ROWB + ((dch ^ bswz(row, CPR)) << 4);
   }
   // pair p of the current item sits in buffer (p + boff) % NBUF; boff carries the
@@ -835,8 +840,10 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   };
   auto dma_part = [&](const Dma& j, int k) __attribute__((always_inline)) {
     if (k < 2 * NDMA) {
-      const int blk = wave + (k >> 1) * NW;
-      dma16((k & 1) ? j.d : j.q, j.buf + (k & 1) * TILE + blk * 1024, dvo[k >> 1], 0);
+      if (wave < NDW) {
+        const int blk = wave + (k >> 1) * NDW;
+        dma16((k & 1) ? j.d : j.q, j.buf + (k & 1) * TILE + blk * 1024, dvo[k >> 1], 0);
+      }
     } else if (wave < 2) {
       dma4(j.r, j.buf + OFF_L + wave * 4 * BMQ, 4 * lane, 0);
     }
@@ -1029,7 +1036,8 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     if (tb + 1 < te && !(pre & 2)) dma_pair(bh0, i0, walk_w(tb + 1, hc, rev, te), bufp(tb + 1));
     if (first && tb + 1 < te) {
       // pair tb has landed once at most pair tb+1's operations are outstanding
-      if (wave < 2) __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA + 1));
+      if (wave >= NDW) __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);  // (no DMA of its own)
+      else if (wave < 2) __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA + 1));
       else __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0 | (2 * NDMA));
     } else {
       __builtin_amdgcn_s_waitcnt(kBwdWaitVmcnt0);
@@ -1119,7 +1127,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   };
   auto stream1 = [&](int t) __attribute__((always_inline)) {
     int dbh, dqi, dpp;
-    const bool dm = dma_at(t + 2, dbh, dqi, dpp);
+    const bool dm = NDW == NW && dma_at(t + 2, dbh, dqi, dpp);  // (role 1 issues DMA only without WALK)
     Dma job;
     if (dm) job = dma_prep(dbh, dqi, dpp, bufp(t + 2));
     const unsigned char* bn = bufp(t + 1);
@@ -1156,7 +1164,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     static_for<0, NT>([&](auto I) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
       if constexpr (i + PD < NT) rot[(i + PD) % (PD + 1)] = rd(i + PD);
-      if constexpr (i % 2 == 0 && i / 2 <= 2 * NDMA)
+      if constexpr (NDW == NW && i % 2 == 0 && i / 2 <= 2 * NDMA)
         if (dm) dma_part(job, i / 2);
       if constexpr (DS1_IN && i < 4) ds_chunk(1, i);
       if constexpr (i == NV / 2) {  // dS is formed: x takes dP(t+1) - Delta
@@ -1668,17 +1676,18 @@ static bool launch_dkdv(const BwdArgs& a) {
   // -6.0 % at B=2 H=16 S=4096 fp16, -3.5 % MQA B=1 H=32 S=4096, -12.6 % B=4 H=32 bf16)
   if constexpr (FA_DKDV_PAIR && D == 128) {
     if (a.rowb) {
-      // one workgroup per CU walks the key tiles (the kernel reads the grid size); the
-      // alternating walk when a K/V head's query heads of Q and dO fill the 4 MiB L2
-      // (backward against the upward walk, D = 128 bf16: B=2 H=32 S=4096 with G = 4
-      // +3.9 %, B=1 H=32 S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %, MHA
-      // S=8192 B=2 H=32 / B=1 H=32 / B=1 H=16 +3.2 / +3.6 / +1.8 %, G = 2 S=4096
-      // B=2 / B=1 / B=4 H=32 +0.0 / +0.6 / +0.5 %; MHA S=4096 (2 MiB) B=4 H=32 -1.0 / -1.1 %)
-      const bool walk = (long long)(a.H / a.Hkv) * a.S * D * 4 >= (4ll << 20);
-      const auto kern = walk ? dkdv_pair_kernel<E, D, BMQ, BNK, true> : dkdv_pair_kernel<E, D, BMQ, BNK, false>;
-      static const int per_cu_up = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, false>, 4 * BNK);
-      static const int per_cu_walk = occupancy_per_cu((const void*)dkdv_pair_kernel<E, D, BMQ, BNK, true>, 4 * BNK);
-      const dim3 pgrid(resident_grid((int)grid.x, walk ? per_cu_walk : per_cu_up));
+      // one workgroup per CU walks the key tiles (the kernel reads the grid size) on the
+      // alternating walk.  Against the upward walk (its WALK = false instance) the
+      // alternating one first paid where a K/V head's query heads of Q and dO fill the
+      // 4 MiB L2 (D = 128 bf16 backward: B=2 H=32 S=4096 with G = 4 +3.9 %, B=1 H=32
+      // S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %, MHA S=8192 B=2 H=32 / B=1 H=32 /
+      // B=1 H=16 +3.2 / +3.6 / +1.8 %; MHA S=4096 B=4 H=32 -1.0 %); with its DMA issued by
+      // the role-0 waves it pays at every size measured (MHA B=4 H=32 S=4096 +0.9 % in three
+      // runs, B=2 / B=1 H=32 S=4096 +0.5 / +1.4 %, B=4 H=32 S=2048 / 1024 +0.2 / +2.2 %,
+      // B=2 H=16 S=2048 +0.5 %, B=2 H=8 S=2048 +0.6 %, B=1 H=8 S=4096 +0.6 %)
+      const auto kern = dkdv_pair_kernel<E, D, BMQ, BNK, true>;
+      static const int per_cu = occupancy_per_cu((const void*)kern, 4 * BNK);
+      const dim3 pgrid(resident_grid((int)grid.x, per_cu));
       hipLaunchKernelGGL(kern, pgrid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
                          (const uint16_t*)a.q, (const uint16_t*)a.k, (const uint16_t*)a.v, (const uint16_t*)a.d_o,
                          a.rowb, (uint16_t*)a.dk, (uint16_t*)a.dv, a.wsk, a.wsv,

@@ -195,15 +195,14 @@ def test_dkdv_split_matches_register_sums(shape):
                                    (2, 8, 2, 3000, 128, "bf16"), (1, 8, 1, 1100, 128, "fp16")],
                          ids=lambda s: "B%dH%dHkv%dS%dD%d-%s" % s)
 def test_dkdv_alternating_walk(shape):
-    """Shapes whose K/V heads' query heads of Q and dO reach 4 MiB take the dK/dV walk whose even
-    rounds run from the last query tile down, with the split's chunks interleaved (partial last
+    """The dK/dV walk (every D = 128 backward with a workspace takes it), whose even rounds run
+    from the last query tile down, with the split's chunks interleaved (partial last
     tiles, splits of 57, 16 and 6 chunks here, bf16 and fp16; the unsplit walk is the full-size
     B2 H32 Hkv8 case): against the fp32 reference, against one workgroup summing each key tile's pairs in registers
     (no workspace), with a smaller split, and bitwise reproducible."""
     from attention import _lib
     from attention.backward.fused_backward import _forward
     B, H, Hkv, S, D, dt = shape
-    assert (H // Hkv) * S * D * 4 > 4 << 20
     q, k, v, do = make(B, H, Hkv, S, D, DTYPES[dt], seed=S + H)
     log(f"dkdv alternating walk {shape}")
     check(q, k, v, do, (128, 64), f"dkdv walk {shape}")
@@ -222,17 +221,17 @@ def test_dkdv_alternating_walk(shape):
 
 @pytest.mark.parametrize("shape", [(1, 4, 1, 2200), (3, 8, 2, 2500), (1, 32, 2, 700), (2, 24, 3, 1500),
                                    (1, 64, 1, 200), (1, 2, 1, 8193), (1, 1, 1, 9000), (4, 16, 4, 2100),
-                                   (1, 2, 2, 8192), (1, 4, 2, 4096)],
+                                   (1, 2, 2, 8192), (1, 4, 2, 4096), (2, 8, 8, 1000), (1, 2, 2, 4096),
+                                   (3, 4, 4, 333), (1, 1, 1, 64)],
                          ids=lambda s: "B%dH%dHkv%dS%d" % s)
 def test_dkdv_alternating_walk_sweep(shape):
-    """More shapes of the alternating dK/dV walk (D = 128 bf16, G from 1 to 64, S from 200 to 9000,
-    splits of 2 to 64 chunks, the 4 MiB threshold itself): equal to one workgroup summing each key
+    """More shapes of the alternating dK/dV walk (D = 128 bf16, G from 1 to 64, S from 64 to 9000,
+    splits of 2 to 64 chunks, MHA shapes small and large): equal to one workgroup summing each key
     tile's pairs in registers up to fp32 summation order, dQ identical."""
     from attention import _lib
     from attention.backward.fused_backward import _forward
     B, H, Hkv, S = shape
     D = 128
-    assert (H // Hkv) * S * D * 4 >= 4 << 20
     q, k, v, do = make(B, H, Hkv, S, D, torch.bfloat16, seed=7 * S + H)
     log(f"dkdv alternating walk sweep {shape}")
     o, lse = _forward(q, k, v, 128, 64)
