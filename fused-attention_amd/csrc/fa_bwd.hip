@@ -648,7 +648,7 @@ void dkdv_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
 // other throughout the iteration.  P of pair t sits in slot t % 2.  The grid holds
 // one workgroup per CU, each walking a fixed share of the key tiles (see the work
 // items below) with the next tile's first pairs loaded under the current one's last.
-template <typename E, int D, int BMQ, int BNK, bool WALK>
+template <typename E, int D, int BMQ, int BNK>
 __global__ __launch_bounds__(4 * BNK)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
@@ -666,11 +666,11 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   constexpr int OFF_L = 2 * TILE;                        // Q | dO | -LSE/c | -Delta
   constexpr int BUFA = (OFF_L + 2 * BMQ * 4 + 1023) / 1024 * 1024;
   constexpr int NBUF = 3;
-  // DMA waves: all eight, or with WALK the four of role 0 (role 1's stream is the longer
-  // one, and on the alternating walk the role-0 DMA measured +1.6 % and +2.2 % at GQA
-  // B=2 H=32 H_kv=8 S=4096 and B=1 H=32 H_kv=4 S=8192; on the upward walk -1.2 % at
-  // B=4 H=32 S=4096)
-  constexpr int NDW = WALK ? NW / 2 : NW;
+  // DMA waves: the four of role 0, whose stream is the shorter one (against all eight
+  // waves: +1.6 % and +2.2 % at GQA B=2 H=32 H_kv=8 S=4096 and B=1 H=32 H_kv=4 S=8192, +0.9 %
+  // at MHA B=4 H=32 S=4096; the same split on the upward walk, the kernel's earlier form,
+  // lost 1.2 % there)
+  constexpr int NDW = NW / 2;
   constexpr int NDMA = NBLK / NDW;
   constexpr int XPS = NKB * 2 * 2 * 64;                  // 16-byte P pieces per slot
   static_assert(TILE % 1024 == 0 && NBLK % NW == 0, "tiles are whole 1 KB DMA blocks, split evenly");
@@ -699,12 +699,12 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   // loaded (a workgroup's start-up, ~6 us of a ~57 us item at B=4 H=32 S=4096 D=128,
   // otherwise leaves its CU idle).
   // An item's pairs: the key tile's walk index w = G (di - i0) + dg covers query tiles
-  // di >= i0 (its diagonal tile) of the G query heads bh0 + dg.  Without WALK, chunk hc
-  // is the range [T hc / nsplit, T (hc+1) / nsplit) of the T = G (nq - i0) indices,
-  // run upward from the diagonal.  With WALK (chosen when a K/V head's G heads of Q
-  // and dO fill the L2), chunk hc takes the w with w % nsplit == hc, and items of
-  // even rounds run their chunk from the last query tile down, odd rounds from the
-  // diagonal up: the slots of an XCD all start an even round at the last query tile,
+  // di >= i0 (its diagonal tile) of the G query heads bh0 + dg; of the T = G (nq - i0)
+  // indices, chunk hc takes the w with w % nsplit == hc.  The walk alternates: items
+  // of even rounds run their chunk from the last query tile down, odd rounds from the
+  // diagonal up (an upward walk of contiguous chunks, its earlier form, read each Q/dO
+  // tile once per key tile where a K/V head's G heads of Q and dO exceed the L2, and
+  // measured at or below this one everywhere): the slots of an XCD all start an even round at the last query tile,
   // and each starts its odd-round item (diagonal two tiles below where its even-round
   // item ended) at the time the others pass that tile, so the XCD's workgroups read
   // the same Q/dO tiles at about the same time and each is fetched about once, not
@@ -735,15 +735,9 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     it.i0 = (it.jt * BNK) / BMQ;
     const int T = G * (nq - it.i0), hc = it.u % nsplit;
     it.hc = hc;
-    if constexpr (WALK) {
-      it.rev = (k & 1) ? 0 : 1;
-      it.tb = 0;
-      it.te = T > hc ? (T - hc + nsplit - 1) / nsplit : 0;
-    } else {
-      it.rev = 0;
-      it.tb = (int)((long long)T * hc / nsplit);
-      it.te = (int)((long long)T * (hc + 1) / nsplit);
-    }
+    it.rev = (k & 1) ? 0 : 1;
+    it.tb = 0;
+    it.te = T > hc ? (T - hc + nsplit - 1) / nsplit : 0;
     return it;
   };
   const int L0 = item_L(0);
@@ -751,7 +745,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
 
   // the current item, as the code below reads it, and the next one (plain scalars:
   // as structs chosen at run time they went to scratch memory)
-  // an item's sequence runs over positions tb .. te-1 (tb = 0 with WALK)
+  // an item's sequence runs over positions tb .. te-1 (tb = 0)
   int u, jt, bh0, i0, hc, rev, tb, te, k0w, n;
   size_t base;
   bool active;
@@ -801,10 +795,9 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     return bufs + __builtin_amdgcn_readfirstlane(((t + boff) % NBUF) * BUFA);
   };
   // position p of an item (chunk ihc, direction irev, positions 0 .. ite-1): walk
-  // index w, i.e. query tile i0 + w / G of query head bh0 + w % G (without WALK, w = p)
+  // index w, i.e. query tile i0 + w / G of query head bh0 + w % G
   auto walk_w = [&](int p, int ihc, int irev, int ite) __attribute__((always_inline)) {
-    if constexpr (WALK) return ihc + (irev ? ite - 1 - p : p) * nsplit;
-    else return p;
+    return ihc + (irev ? ite - 1 - p : p) * nsplit;
   };
   auto qtile = [&](int p) __attribute__((always_inline)) { return i0 + walk_w(p, hc, rev, te) / G; };
   // the pair's DMA in 2 NDMA + 1 parts: part 2x / 2x+1 = block x of the Q / dO tile,
@@ -971,14 +964,9 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
   int E0 = 0, E1 = 0;
   auto set_edges = [&]() __attribute__((always_inline)) {
     const int TEw = G * min(2, nq - i0);                // walk indices of the edge pairs
-    if constexpr (WALK) {
-      const int ne = TEw > hc ? (TEw - hc + nsplit - 1) / nsplit : 0;
-      E0 = rev ? 0 : ne;
-      E1 = rev ? te - ne : te;
-    } else {
-      E0 = min(te, TEw);
-      E1 = te;
-    }
+    const int ne = TEw > hc ? (TEw - hc + nsplit - 1) / nsplit : 0;
+    E0 = rev ? 0 : ne;
+    E1 = rev ? te - ne : te;
   };
   // pair t+1 has landed, P(t) is visible, and nobody reads pair t-1's buffer or
   // slot (t+1) % 2 any more
@@ -1125,11 +1113,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  auto stream1 = [&](int t) __attribute__((always_inline)) {
-    int dbh, dqi, dpp;
-    const bool dm = NDW == NW && dma_at(t + 2, dbh, dqi, dpp);  // (role 1 issues DMA only without WALK)
-    Dma job;
-    if (dm) job = dma_prep(dbh, dqi, dpp, bufp(t + 2));
+  auto stream1 = [&](int t) __attribute__((always_inline)) {  // (role 1 issues no DMA)
     const unsigned char* bn = bufp(t + 1);
     const unsigned char* bc = bufp(t);
     u32x4 w[2][2], bop[2][2];
@@ -1164,8 +1148,6 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     static_for<0, NT>([&](auto I) __attribute__((always_inline)) {
       constexpr int i = decltype(I)::value;
       if constexpr (i + PD < NT) rot[(i + PD) % (PD + 1)] = rd(i + PD);
-      if constexpr (NDW == NW && i % 2 == 0 && i / 2 <= 2 * NDMA)
-        if (dm) dma_part(job, i / 2);
       if constexpr (DS1_IN && i < 4) ds_chunk(1, i);
       if constexpr (i == NV / 2) {  // dS is formed: x takes dP(t+1) - Delta
         x[0] = load_rows(reinterpret_cast<const float*>(bn + lo), 0);
@@ -1231,7 +1213,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     for (int k = 0;; ++k) {
       begin_item(k);
       // (E1f: the full pairs whose successor, if any, is full as well)
-      const int E1f = (WALK && E1 < te) ? E1 - 1 : E1;
+      const int E1f = E1 < te ? E1 - 1 : E1;
       int t = tb;
       for (; t < E0; ++t) step_mv(t, BTag<false>{});  // leading edge pairs
       for (; t + 2 < E1; t += 2) {
@@ -1241,8 +1223,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
         stream0(t + 1, pkn, pk);
       }
       for (; t < E1f; ++t) step_mv(t, BTag<true>{});
-      if constexpr (WALK)
-        for (; t < te; ++t) step_mv(t, BTag<false>{});  // trailing edge pairs
+      for (; t < te; ++t) step_mv(t, BTag<false>{});  // trailing edge pairs
       epilogue();
       if (!has_next) break;
       next_item();
@@ -1255,7 +1236,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
     };
     for (int k = 0;; ++k) {
       begin_item(k);
-      const int E1f = (WALK && E1 < te) ? E1 - 1 : E1;
+      const int E1f = E1 < te ? E1 - 1 : E1;
       int t = tb;
       for (; t < E0; ++t) step1(t, BTag<false>{});
       for (; t + 1 < E1; ++t) {
@@ -1263,8 +1244,7 @@ void dkdv_pair_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict
         stream1(t);
       }
       for (; t < E1f; ++t) step1(t, BTag<true>{});
-      if constexpr (WALK)
-        for (; t < te; ++t) step1(t, BTag<false>{});
+      for (; t < te; ++t) step1(t, BTag<false>{});
       epilogue();
       if (!has_next) break;
       next_item();
@@ -1677,7 +1657,7 @@ static bool launch_dkdv(const BwdArgs& a) {
   if constexpr (FA_DKDV_PAIR && D == 128) {
     if (a.rowb) {
       // one workgroup per CU walks the key tiles (the kernel reads the grid size) on the
-      // alternating walk.  Against the upward walk (its WALK = false instance) the
+      // alternating walk.  Against the upward walk (the kernel's earlier form) the
       // alternating one first paid where a K/V head's query heads of Q and dO fill the
       // 4 MiB L2 (D = 128 bf16 backward: B=2 H=32 S=4096 with G = 4 +3.9 %, B=1 H=32
       // S=4096 MQA +10.3 %, B=1 H=32 S=8192 G = 8 +7.6 %, MHA S=8192 B=2 H=32 / B=1 H=32 /
@@ -1685,7 +1665,7 @@ static bool launch_dkdv(const BwdArgs& a) {
       // the role-0 waves it pays at every size measured (MHA B=4 H=32 S=4096 +0.9 % in three
       // runs, B=2 / B=1 H=32 S=4096 +0.5 / +1.4 %, B=4 H=32 S=2048 / 1024 +0.2 / +2.2 %,
       // B=2 H=16 S=2048 +0.5 %, B=2 H=8 S=2048 +0.6 %, B=1 H=8 S=4096 +0.6 %)
-      const auto kern = dkdv_pair_kernel<E, D, BMQ, BNK, true>;
+      const auto kern = dkdv_pair_kernel<E, D, BMQ, BNK>;
       static const int per_cu = occupancy_per_cu((const void*)kern, 4 * BNK);
       const dim3 pgrid(resident_grid((int)grid.x, per_cu));
       hipLaunchKernelGGL(kern, pgrid, dim3(4 * BNK), 0, (hipStream_t)a.stream,
