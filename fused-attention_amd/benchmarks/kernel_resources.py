@@ -69,7 +69,7 @@ HEADER = [
     "\"Occupancy\" is the compiler's waves per SIMD for the registers and LDS.  Template arguments:",
     "`fwd_kernel<E, D, rows per head, keys per tile, heads per workgroup, LSE>`,",
     "`dq_kernel<E, D, rows, keys>`, `dkdv_kernel<E, D, query rows per tile, keys per workgroup, per-row terms>`,",
-    "`dkdv_pair_kernel<E, D, query rows per tile, keys per workgroup, alternating walk>` (D = 128 only).",
+    "`dkdv_pair_kernel<E, D, query rows per tile, keys per workgroup>` (D = 128 only).",
     "",
 ]
 
