@@ -117,16 +117,16 @@ int dq_block_m(int block_m, int D) { return (block_m == 64 && D >= 64) ? 128 : b
 // persistent workgroup per CU that walks its items; the one-wave kernel (D <= 64) two
 // workgroups per CU, one per item.  Measured (profiles/dkdv_split_study.md, dK/dV +
 // reduction, us, the rule's choice first):
-//   paired: MQA B=1 H=32 S=4096 D=128, 16 / 8 / 32: 261 / 401 / 294; MHA B=1 H=4 S=8192,
-//   2 / 1 / 4: 143 / 202 / 161; MHA B=1 H=8 S=4096, 2 / 1 / 4: 86 / 98 / 106; GQA B=1 H=32
-//   H_kv=4 S=8192, 2 / 1 / 4: 977 / 1542 / 1000; B=1 H=8 H_kv=1 S=16384, 8 / 4 / 16: 972 /
-//   1264 / 1022;
-//   one-wave: MQA B=1 H=32 S=4096 D=64, 32 / 16 / 64: 181 / 211 / 191; MHA B=1 H=16 S=4096
-//   D=64, 2 / 1 / 4: 97 / 107 / 113; B=2 H=16 S=4096 D=64, 1 / 2: 155 / 188; MQA B=1 H=32
-//   S=16384 D=64, 16 / 8 / 32: 2017 / 2140 / 2053.
+//   paired: MQA B=1 H=32 S=4096 D=128, 16 / 8 / 32: 264 / 392 / 291; MHA B=1 H=4 S=8192,
+//   2 / 1 / 4: 146 / 201 / 163; MHA B=1 H=8 S=4096, 2 / 1 / 4: 87 / 98 / 106; GQA B=1 H=32
+//   H_kv=4 S=8192, 2 / 1 / 4: 960 / 1495 / 978; B=1 H=8 H_kv=1 S=16384, 8 / 4 / 16: 972 /
+//   1196 / 1006;
+//   one-wave: MQA B=1 H=32 S=4096 D=64, 32 / 16 / 64: 185 / 218 / 191; MHA B=1 H=16 S=4096
+//   D=64, 2 / 1 / 4: 98 / 108 / 113; B=2 H=16 S=4096 D=64, 1 / 2: 158 / 187; MQA B=1 H=32
+//   S=16384 D=64, 16 / 8 / 32: 2119 / 2224 / 2155.
 // (The previous rule, 2 x CU items per 4096 keys for both kernels, chose 4 for MHA
 // B=1 H=4 S=8192 and for the GQA shape, 16 for B=1 H=8 H_kv=1 and for MQA S=4096 D=64, and
-// 1 for MHA B=1 H=16 D=64: 13, 2, 5, 16 and 10 % slower.)  D = 32 runs the one-wave kernel
+// 1 for MHA B=1 H=16 D=64: 12, 2, 4, 18 and 10 % slower.)  D = 32 runs the one-wave kernel
 // and takes its rule unmeasured.
 int dkdv_target_workgroups(int S, int D) {
   const int slots = cu_count() * (D == 128 ? 1 : 2);
