@@ -21,20 +21,42 @@ CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
          "-packed-fp32-ops", "-fvisibility=hidden", "-Wno-unused-command-line-argument",
          "-Rpass-analysis=kernel-resource-usage", "-c", "-o", os.devnull]
+ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 SLICES = [(e, d) for e in ("bf16", "f16") for d in (128, 64, 32)]
 FIELDS = ["VGPRs", "AGPRs", "TotalSGPRs", "ScratchSize [bytes/lane]", "Occupancy [waves/SIMD]",
           "SGPRs Spill", "VGPRs Spill", "LDS Size [bytes/block]"]
 
 
-def compile_slice(hipcc, family, etype, D):
+def objects():
+    """(family, etype, D, forward part, scheduler flags) of every object the Makefile builds:
+    the backward slices under max-ILP, the D = 128 forward as its one-head part (max-ILP)
+    and its grouped part, the other forward slices whole."""
+    out = []
+    for e, d in SLICES:
+        if d == 128:
+            out += [("fwd", e, d, 1, ILP), ("fwd", e, d, 2, [])]
+        else:
+            out.append(("fwd", e, d, 0, []))
+        out.append(("bwd", e, d, 0, ILP))
+    return out
+
+
+def compile_slice(hipcc, family, etype, D, part, sched):
     et = "fa::BF16" if etype == "bf16" else "fa::F16"
-    table = f"-DFA_FWD_TABLE=fa_fwd_table_{etype}_{D}" if family == "fwd" else f"-DFA_BWD_TABLE=fa_bwd_table_{etype}_{D}"
+    if family == "fwd":
+        defs = [f"-DFA_FWD_PART={part}", f"-DFA_FWD_TABLE=fa_fwd_table_{etype}_{D}",
+                f"-DFA_FWD_TABLE_GROUPED=fa_fwd_table_{etype}_{D}_grouped"]
+    else:
+        defs = [f"-DFA_BWD_TABLE=fa_bwd_table_{etype}_{D}"]
     src = os.path.join(CSRC, f"fa_{family}.hip")
-    r = subprocess.run([hipcc, *FLAGS, f"-DFA_ETYPE={et}", f"-DFA_D={D}", table, src],
+    r = subprocess.run([hipcc, *FLAGS, *sched, f"-DFA_ETYPE={et}", f"-DFA_D={D}", *defs, src],
                        capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"{src} ({etype}, D={D}) failed:\n{r.stderr[-2000:]}")
-    return parse(r.stderr)
+        raise RuntimeError(f"{src} ({etype}, D={D}, part {part}) failed:\n{r.stderr[-2000:]}")
+    kernels = parse(r.stderr)
+    for k in kernels.values():
+        k["Scheduler"] = "max-ilp" if sched else "default"
+    return kernels
 
 
 def demangle(name):
@@ -65,8 +87,9 @@ HEADER = [
     "",
     "    cd fused-attention_amd && python3 -m benchmarks.kernel_resources --out ../profiles/kernel_resources.md",
     "",
-    "Each slice of `csrc/` compiled as the Makefile does with `-Rpass-analysis=kernel-resource-usage`;",
-    "\"Occupancy\" is the compiler's waves per SIMD for the registers and LDS.  Template arguments:",
+    "Each object of `csrc/` compiled as the Makefile does with `-Rpass-analysis=kernel-resource-usage`;",
+    "\"Occupancy\" is the compiler's waves per SIMD for the registers and LDS; \"Scheduler\" the machine",
+    "scheduling strategy its object is built under.  Template arguments:",
     "`fwd_kernel<E, D, rows per head, keys per tile, heads per workgroup, LSE>`,",
     "`dq_kernel<E, D, rows, keys>`, `dkdv_kernel<E, D, query rows per tile, keys per workgroup, per-row terms>`,",
     "`dkdv_pair_kernel<E, D, query rows per tile, keys per workgroup>` (D = 128 only).",
@@ -79,14 +102,15 @@ def main(argv=None):
     p.add_argument("--hipcc", default="/opt/rocm/bin/hipcc")
     p.add_argument("--out", default="")
     args = p.parse_args(argv)
-    jobs = [(f, e, d) for f in ("fwd", "bwd") for e, d in SLICES]
+    jobs = sorted(objects(), key=lambda j: (j[0] != "fwd", j[1], -j[2], j[3]))
     with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         results = list(ex.map(lambda j: compile_slice(args.hipcc, *j), jobs))
-    L = HEADER + ["| kernel | " + " | ".join(FIELDS) + " |", "|---|" + "---|" * len(FIELDS)]
+    cols = FIELDS + ["Scheduler"]
+    L = HEADER + ["| kernel | " + " | ".join(cols) + " |", "|---|" + "---|" * len(cols)]
     for kernels in results:
         for name in sorted(kernels, key=demangle):
             k = kernels[name]
-            L.append(f"| `{demangle(name)}` | " + " | ".join(k.get(f, "-") for f in FIELDS) + " |")
+            L.append(f"| `{demangle(name)}` | " + " | ".join(k.get(f, "-") for f in cols) + " |")
     text = "\n".join(L) + "\n"
     if args.out:
         with open(args.out, "w") as f:

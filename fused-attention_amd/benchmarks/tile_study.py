@@ -11,7 +11,7 @@ counter passes, each in a child process of its own) and writes, per variant: ker
 time, achieved TFLOP/s against the dense MFMA peak, algorithmic HBM GB/s, MFMA busy,
 VALU/MFMA co-execution, LDS activity and bank-conflict cycles, instructions per MFMA
 and the wave-wait fraction.  Registers, LDS and the waves per SIMD they allow are
-compile-time facts: `make -C csrc resources` prints the compiler's own figures.  The
+compile-time facts: `python -m benchmarks.kernel_resources` prints the compiler's own figures.  The
 reference backs its tile choice the same way, with one profiler run per tile
 (profiling/3_tile_study/README.md:8-19).
 

@@ -449,22 +449,46 @@ static int launch_fwd(const FwdArgs& a) {
   return hipGetLastError() == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
+// A slice builds as one object (FA_FWD_PART 0) or, where its instances want different
+// machine schedulers, as two: part 1 the one-head instances and the slice's table, part 2
+// the instances of two and four heads per workgroup, whose table part 1 calls for GQA.
+// The D = 128 slices split so (the Makefile): the one-head kernel runs 0.9-2.2 % faster under
+// the compiler's max-ILP scheduling strategy (B=4 H=32 S=4096 bf16, B=2 H=8 S=8192 fp16),
+// the grouped ones 0.5-1.7 % slower (GQA B=2 H=32 H_kv=8 S=4096 / 8192, B=1 H=32 H_kv=4
+// S=8192); at D <= 64 every instance runs slower under it (-1.8 to -4.6 %), so those slices
+// stay whole under the default strategy.  Outputs are bitwise equal either way.
+#ifndef FA_FWD_PART
+#define FA_FWD_PART 0
+#endif
+
 // Dispatch over the compile-time parameters of one (element type, D) slice.
 template <typename E, int D>
 static FwdFn pick_fwd(int bm, int bn, int gh, bool lse) {
 #define FA_CASE(BM_, BN_, GH_)                                                          \
   if (bm == BM_ && bn == BN_ && gh == GH_)                                             \
     return lse ? launch_fwd<E, D, BM_, BN_, GH_, true> : launch_fwd<E, D, BM_, BN_, GH_, false>;
+#if FA_FWD_PART != 2
   FA_CASE(64, 64, 1) FA_CASE(64, 128, 1) FA_CASE(128, 64, 1) FA_CASE(128, 128, 1)
+#endif
+#if FA_FWD_PART != 1
   FA_CASE(64, 64, 2) FA_CASE(64, 128, 2) FA_CASE(128, 64, 2)
   FA_CASE(64, 64, 4)
+#endif
 #undef FA_CASE
   return nullptr;
 }
 
 }  // namespace fa
 
-// FA_ETYPE (fa::F16 / fa::BF16), FA_D and FA_FWD_TABLE come from the build.
+// FA_ETYPE (fa::F16 / fa::BF16), FA_D and FA_FWD_TABLE come from the build; part 1 also
+// takes FA_FWD_TABLE_GROUPED, the table part 2 was built under.
+#if FA_FWD_PART == 1
+extern "C" FA_HIDDEN fa::FwdFn FA_FWD_TABLE_GROUPED(int bm, int bn, int gh, int lse);
+extern "C" FA_HIDDEN fa::FwdFn FA_FWD_TABLE(int bm, int bn, int gh, int lse) {
+  return gh == 1 ? fa::pick_fwd<FA_ETYPE, FA_D>(bm, bn, gh, lse != 0) : FA_FWD_TABLE_GROUPED(bm, bn, gh, lse);
+}
+#else
 extern "C" FA_HIDDEN fa::FwdFn FA_FWD_TABLE(int bm, int bn, int gh, int lse) {
   return fa::pick_fwd<FA_ETYPE, FA_D>(bm, bn, gh, lse != 0);
 }
+#endif
