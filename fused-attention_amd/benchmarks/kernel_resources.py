@@ -21,24 +21,37 @@ CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
          "-packed-fp32-ops", "-fvisibility=hidden", "-Wno-unused-command-line-argument",
          "-Rpass-analysis=kernel-resource-usage", "-c", "-o", os.devnull]
-ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
 SLICES = [(e, d) for e in ("bf16", "f16") for d in (128, 64, 32)]
 FIELDS = ["VGPRs", "AGPRs", "TotalSGPRs", "ScratchSize [bytes/lane]", "Occupancy [waves/SIMD]",
           "SGPRs Spill", "VGPRs Spill", "LDS Size [bytes/block]"]
 
 
+def makefile_sched():
+    """The Makefile's machine-scheduler options per object group ({variable: [flags]})."""
+    text = open(os.path.join(CSRC, "Makefile")).read()
+    raw = dict(re.findall(r"^(ILP|SCHED_\w+)\s*[:?]?=[ \t]*(.*)$", text, re.M))
+    return {k: v.replace("$(ILP)", raw.get("ILP", "")).split() for k, v in raw.items()}
+
+
 def objects():
     """(family, etype, D, forward part, scheduler flags) of every object the Makefile builds:
-    the backward slices under max-ILP, the D = 128 forward as its one-head part (max-ILP)
-    and its grouped part, the other forward slices whole."""
+    the D = 128 forward as its one-head part and its grouped part, the other forward slices
+    whole, the backward per slice, each under its group's scheduler options."""
+    sch = makefile_sched()
     out = []
     for e, d in SLICES:
         if d == 128:
-            out += [("fwd", e, d, 1, ILP), ("fwd", e, d, 2, [])]
+            out += [("fwd", e, d, 1, sch["SCHED_FWD1"]), ("fwd", e, d, 2, sch["SCHED_FWDG"]),
+                    ("bwd", e, d, 0, sch["SCHED_BWD128"])]
         else:
-            out.append(("fwd", e, d, 0, []))
-        out.append(("bwd", e, d, 0, ILP))
+            out += [("fwd", e, d, 0, sch["SCHED_FWD"]), ("bwd", e, d, 0, sch["SCHED_BWD"])]
     return out
+
+
+def sched_name(flags):
+    """Short name of a scheduler option list: 'max-ilp, topdown', 'bottomup', 'default'."""
+    names = [f.split("=", 1)[1] for f in flags if "=" in f]
+    return ", ".join(names) if names else "default"
 
 
 def compile_slice(hipcc, family, etype, D, part, sched):
@@ -55,7 +68,7 @@ def compile_slice(hipcc, family, etype, D, part, sched):
         raise RuntimeError(f"{src} ({etype}, D={D}, part {part}) failed:\n{r.stderr[-2000:]}")
     kernels = parse(r.stderr)
     for k in kernels.values():
-        k["Scheduler"] = "max-ilp" if sched else "default"
+        k["Scheduler"] = sched_name(sched)
     return kernels
 
 
@@ -89,7 +102,8 @@ HEADER = [
     "",
     "Each object of `csrc/` compiled as the Makefile does with `-Rpass-analysis=kernel-resource-usage`;",
     "\"Occupancy\" is the compiler's waves per SIMD for the registers and LDS; \"Scheduler\" the machine",
-    "scheduling strategy its object is built under.  Template arguments:",
+    "scheduler options its object is built under (the Makefile's `SCHED_*`: strategy, pre-RA direction).",
+    "Template arguments:",
     "`fwd_kernel<E, D, rows per head, keys per tile, heads per workgroup, LSE>`,",
     "`dq_kernel<E, D, rows, keys>`, `dkdv_kernel<E, D, query rows per tile, keys per workgroup, per-row terms>`,",
     "`dkdv_pair_kernel<E, D, query rows per tile, keys per workgroup>` (D = 128 only).",
