@@ -44,7 +44,7 @@ SIGNATURES = {
     "fa_fwd_exact": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _F, _I, _I, _I, _VP]),
     "fa_bwd_gqa_exact": (_I, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
                               _I, _I, _I, _I, _I, _I, _F, _F, _I, _I, _I, _VP, ctypes.c_size_t, _VP]),
-    "fa_fwd_heads_per_wg": (_I, [_I, _I, _I, _I, _I, _I]),
+    "fa_fwd_heads_per_wg": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "fa_fwd_rows_per_wg": (_I, [_I, _I, _I, _I]),
     "fa_bwd_dq_rows_per_wg": (_I, [_I, _I]),
     "fa_bwd_dkdv_split": (_I, [_I, _I, _I, _I, _I]),

@@ -77,19 +77,19 @@ int check_common(int B, int H, int S, int D, int dtype, int block_m, int block_n
 using fa::cu_count;
 using fa::kMaxDevices;
 
-// Forward query heads per workgroup for this launch: heads_per_wg's choice, but
-// four heads (64-row tiles) drop to two when the grid would hold fewer than four
-// workgroups per CU, where the heavy-first order cannot balance the causal
-// triangle (B=2 H=8 H_kv=1 S=8192 fp16, tile 64x64: D=128 0.328 -> 0.288 ms,
-// D=32 0.175 -> 0.123 ms; at B=2 H=32 H_kv=8, 2048 workgroups, four stay 3 %
-// faster).  Two heads of 64 rows still hold two waves per SIMD.  Re-measured on the
-// current kernel (profiles/tile_study_mha_gqa_bwd.md): B=1 H=16 H_kv=4 S=4096 D=128
-// (one workgroup per CU at four heads) two heads 869 TFLOP/s, four 711; B=2 H=8
-// H_kv=1 S=8192 (two per CU) two / four heads D=32 646 / 604, D=64 891 / 907, D=128
-// 1014 / 1098: mixed at two workgroups per CU, kept.
-int fwd_heads_per_wg(int B, int H, int group, int S, int block_m, int block_n) {
+// Forward query heads per workgroup for this launch: heads_per_wg's choice, but four
+// heads (64-row tiles) drop to two where the grid would leave the co-resident pair of
+// workgroups per CU short: below two workgroups per CU, and at D = 32 below four, where
+// the heavy-first order cannot balance the causal triangle with the fewer, longer
+// workgroups.  Two heads of 64 rows still hold two waves per SIMD.  Measured
+// (profiles/tile_study_mha_gqa_bwd.md, TFLOP/s of two / four heads): B=1 H=16 H_kv=4
+// S=4096 D=128 (one workgroup per CU at four heads) 864 / 754; B=2 H=8 H_kv=1 S=8192 fp16
+// (two per CU) D=128 1045 / 1134, D=64 899 / 915, D=32 650 / 602; the study's run before
+// it read the same order (D=128 990 / 1053, D=64 868 / 897, D=32 662 / 629).
+int fwd_heads_per_wg(int B, int H, int group, int S, int D, int block_m, int block_n) {
   int gh = heads_per_wg(group, block_m, block_n);
-  if (gh == 4 && (long long)B * (H / 4) * ((S + block_m - 1) / block_m) < 4LL * cu_count()) gh = 2;
+  const long long wgs = (long long)B * (H / 4) * ((S + block_m - 1) / block_m);
+  if (gh == 4 && wgs < (D <= 32 ? 4LL : 2LL) * cu_count()) gh = 2;
   return gh;
 }
 
@@ -117,16 +117,16 @@ int dq_block_m(int block_m, int D) { return (block_m == 64 && D >= 64) ? 128 : b
 // persistent workgroup per CU that walks its items; the one-wave kernel (D <= 64) two
 // workgroups per CU, one per item.  Measured (profiles/dkdv_split_study.md, dK/dV +
 // reduction, us, the rule's choice first):
-//   paired: MQA B=1 H=32 S=4096 D=128, 16 / 8 / 32: 264 / 392 / 291; MHA B=1 H=4 S=8192,
-//   2 / 1 / 4: 146 / 201 / 163; MHA B=1 H=8 S=4096, 2 / 1 / 4: 87 / 98 / 106; GQA B=1 H=32
-//   H_kv=4 S=8192, 2 / 1 / 4: 960 / 1495 / 978; B=1 H=8 H_kv=1 S=16384, 8 / 4 / 16: 972 /
-//   1196 / 1006;
-//   one-wave: MQA B=1 H=32 S=4096 D=64, 32 / 16 / 64: 185 / 218 / 191; MHA B=1 H=16 S=4096
-//   D=64, 2 / 1 / 4: 98 / 108 / 113; B=2 H=16 S=4096 D=64, 1 / 2: 158 / 187; MQA B=1 H=32
-//   S=16384 D=64, 16 / 8 / 32: 2119 / 2224 / 2155.
+//   paired: MQA B=1 H=32 S=4096 D=128, 16 / 8 / 32: 253 / 377 / 280; MHA B=1 H=4 S=8192,
+//   2 / 1 / 4: 140 / 197 / 160; MHA B=1 H=8 S=4096, 2 / 1 / 4: 84 / 95 / 105; GQA B=1 H=32
+//   H_kv=4 S=8192, 2 / 1 / 4: 913 / 1427 / 937; B=1 H=8 H_kv=1 S=16384, 8 / 4 / 16: 920 /
+//   1170 / 965;
+//   one-wave: MQA B=1 H=32 S=4096 D=64, 32 / 16 / 64: 179 / 212 / 188; MHA B=1 H=16 S=4096
+//   D=64, 2 / 1 / 4: 98 / 108 / 113; B=2 H=16 S=4096 D=64, 1 / 2: 155 / 186; MQA B=1 H=32
+//   S=16384 D=64, 16 / 8 / 32: 2039 / 2160 / 2074.
 // (The previous rule, 2 x CU items per 4096 keys for both kernels, chose 4 for MHA
 // B=1 H=4 S=8192 and for the GQA shape, 16 for B=1 H=8 H_kv=1 and for MQA S=4096 D=64, and
-// 1 for MHA B=1 H=16 D=64: 12, 2, 4, 18 and 10 % slower.)  D = 32 runs the one-wave kernel
+// 1 for MHA B=1 H=16 D=64: 14, 3, 5, 18 and 10 % slower.)  D = 32 runs the one-wave kernel
 // and takes its rule unmeasured.
 int dkdv_target_workgroups(int S, int D) {
   const int slots = cu_count() * (D == 128 ? 1 : 2);
@@ -209,7 +209,7 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   if (st != FA_OK) return st;
   if (H_kv <= 0 || H_kv > H || H % H_kv != 0) return FA_ERR_DIMS;
   if (!q || !k || !v || !o) return FA_ERR_NULL;
-  const int gh = fwd_heads_per_wg(B, H, H / H_kv, S, block_m, block_n);
+  const int gh = fwd_heads_per_wg(B, H, H / H_kv, S, D, block_m, block_n);
   fa::FwdFn fn = fwd_table(dtype, D, fwd_block_m(block_m, block_n, D, gh), block_n, gh, lse != nullptr);
   if (!fn) return FA_ERR_UNSUPPORTED;
   fa::FwdArgs a{q, k, v, o, lse, B, H, H_kv, S, D, scale_log2, hip_stream};
@@ -333,10 +333,11 @@ int fa_bwd_gqa_exact(const void* q, const void* k, const void* v, const void* o,
   return fn(a);
 }
 
-int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int block_m, int block_n) {
+int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int D, int block_m, int block_n) {
   if (B <= 0 || H <= 0 || S <= 0 || H_kv <= 0 || H_kv > H || H % H_kv != 0) return 0;
+  if (D != 32 && D != 64 && D != 128) return 0;
   if (!tile_ok(block_m) || !tile_ok(block_n)) return 0;
-  return fwd_heads_per_wg(B, H, H / H_kv, S, block_m, block_n);
+  return fwd_heads_per_wg(B, H, H / H_kv, S, D, block_m, block_n);
 }
 
 int fa_fwd_rows_per_wg(int block_m, int block_n, int D, int heads_per_wg) {

@@ -180,7 +180,7 @@ FA_API int fa_bwd_gqa_exact(const void* q, const void* k, const void* v, const v
                      int B, int H, int H_kv, int S, int D, int dtype, float scale_log2, float sm_scale,
                      int dq_block_m, int dq_block_n, int nsplit, void* workspace, size_t workspace_bytes,
                      void* hip_stream);
-FA_API int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int block_m, int block_n);
+FA_API int fa_fwd_heads_per_wg(int B, int H, int H_kv, int S, int D, int block_m, int block_n);
 FA_API int fa_fwd_rows_per_wg(int block_m, int block_n, int D, int heads_per_wg);
 FA_API int fa_bwd_dq_rows_per_wg(int block_m, int D);
 FA_API int fa_bwd_dkdv_split(int B, int H, int H_kv, int S, int D);

@@ -226,11 +226,15 @@ def test_exact_shape_entries_and_rule_queries(lib):
     assert lib.fa_fwd_rows_per_wg(64, 128, 64, 1) == 64 and lib.fa_fwd_rows_per_wg(64, 64, 32, 2) == 64
     assert lib.fa_bwd_dq_rows_per_wg(64, 128) == 128 and lib.fa_bwd_dq_rows_per_wg(64, 64) == 128
     assert lib.fa_bwd_dq_rows_per_wg(64, 32) == 64 and lib.fa_bwd_dq_rows_per_wg(128, 32) == 128
-    assert lib.fa_fwd_heads_per_wg(4, 32, 32, 4096, 128, 64) == 1
-    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 64, 64) == 4
-    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 64) == 2
-    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 1024, 64, 64) == 2     # 4 -> 2: under 4 workgroups per CU
-    assert lib.fa_fwd_heads_per_wg(1, 32, 1, 16384, 64, 128) == 2
+    assert lib.fa_fwd_heads_per_wg(4, 32, 32, 4096, 128, 128, 64) == 1
+    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 64, 64) == 4
+    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 128, 64) == 2
+    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 1024, 128, 64, 64) == 2   # 4 -> 2: under 2 workgroups per CU
+    assert lib.fa_fwd_heads_per_wg(1, 16, 4, 4096, 128, 64, 64) == 2  # one per CU at four heads
+    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 8192, 128, 64, 64) == 4   # two per CU: four stay
+    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 8192, 64, 64, 64) == 4
+    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 8192, 32, 64, 64) == 2    # D = 32: under 4 per CU
+    assert lib.fa_fwd_heads_per_wg(1, 32, 1, 16384, 64, 64, 128) == 2
     # dK/dV split: two items per workgroup slot (the paired D = 128 kernel one slot per CU, the
     # one-wave kernel two), one round more per 8192 keys; no split under 64 pairs per key tile
     assert lib.fa_bwd_dkdv_split(4, 32, 32, 4096, 128) == 1
@@ -243,5 +247,6 @@ def test_exact_shape_entries_and_rule_queries(lib):
     assert lib.fa_bwd_dkdv_split(1, 16, 16, 4096, 64) == 2     # 512 key tiles, target 1024
     assert lib.fa_bwd_dkdv_split(2, 16, 16, 4096, 64) == 1
     assert lib.fa_bwd_dkdv_split(2, 8, 8, 2048, 128) == 1      # 32 pairs per key tile
-    assert lib.fa_fwd_heads_per_wg(0, 32, 8, 4096, 64, 64) == 0 and lib.fa_bwd_dkdv_split(1, 4, 3, 64, 128) == 0
+    assert lib.fa_fwd_heads_per_wg(0, 32, 8, 4096, 128, 64, 64) == 0 and lib.fa_bwd_dkdv_split(1, 4, 3, 64, 128) == 0
+    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 4096, 48, 64, 64) == 0
     assert lib.fa_bwd_dkdv_split(1, 4, 4, 64, 48) == 0
