@@ -49,8 +49,8 @@ fa::BwdFn bwd_table(int dtype, int D, int bm, int bn) {
 // 128-key tiles a wave holds two 128-key score tiles in flight and needs more
 // than the 256 VGPRs of two waves per SIMD, so the workgroup stays at 4 waves.
 // Counters (profiles/tile_study_mha_gqa_bwd.md, GQA B=2 H=32 H_kv=8 S=8192 D=128):
-// one head of 64 rows 905 TFLOP/s, MFMA busy 48.7 %; two heads 1179 / 72.7 %; four
-// heads 1198 / 64.6 %.
+// one head of 64 rows 898 TFLOP/s, MFMA busy 48.2 %; two heads 1185 / 71.4 %; four
+// heads 1236 / 68.4 %.
 int heads_per_wg(int group, int block_m, int block_n) {
   int cap = (block_n == 128 ? 128 : 256) / block_m;  // waves / (block_m / 32)
   if (cap > kMaxGroupHeadsPerWg) cap = kMaxGroupHeadsPerWg;
@@ -99,15 +99,16 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int D, int block_m, int blo
 // its K and V tiles double-buffered in LDS it gets one wave per SIMD or less;
 // where that is measured slower, tile_m = 64 runs as 128-row workgroups.
 // Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows
-// (profiles/tile_study_mha_gqa_bwd.md): tile_n = 64: D=128 828 -> 1087 (MFMA busy
-// 43.9 -> 64.8 %: a 64-row workgroup holds one wave per SIMD), D=64 681 -> 943, D=32
-// 443 -> 677; tile_n = 128: D=128 475 -> 761 (D <= 64 about equal, so left).  dQ, D >= 64:
-// 64 -> 128 rows at D=128 868 -> 1138 (MFMA busy 43.4 -> 61.1 %), at D=64 945 -> 979 with
-// 64-key tiles and 716 -> 1008 with 128-key tiles; at D=32 729 -> 772 (left literal).
+// (profiles/tile_study_mha_gqa_bwd.md): tile_n = 64: D=128 845 -> 1106 (MFMA busy
+// 43.9 -> 66.8 %: a 64-row workgroup holds one wave per SIMD), D=64 649 -> 922, D=32
+// 441 -> 675; tile_n = 128: D=128 464 -> 775 (D <= 64 about equal, so left).  dQ, every
+// head dim: 64 -> 128 rows at D=128 870 -> 1144 (MFMA busy 42.4 -> 62.2 %), at D=64
+// 973 -> 1003 with 64-key tiles and 681 -> 1019 with 128-key tiles, at D=32 739 -> 794
+// (the D = 32 backward +0.9-2.3 % at four shapes in A/B runs, -0.3 % at B=2 H=16 S=4096).
 int fwd_block_m(int block_m, int block_n, int D, int gh) {
   return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
 }
-int dq_block_m(int block_m, int D) { return (block_m == 64 && D >= 64) ? 128 : block_m; }
+int dq_block_m(int block_m, int /*D*/) { return block_m == 64 ? 128 : block_m; }
 
 // Work items (key-tile chunks) the dK/dV kernel should have for its heavy-first order
 // to balance: two per workgroup slot the GPU holds at once, and one round more per
