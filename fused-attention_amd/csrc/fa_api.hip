@@ -86,10 +86,19 @@ using fa::kMaxDevices;
 // S=4096 D=128 (one workgroup per CU at four heads) 864 / 754; B=2 H=8 H_kv=1 S=8192 fp16
 // (two per CU) D=128 1045 / 1134, D=64 899 / 915, D=32 650 / 602; the study's run before
 // it read the same order (D=128 990 / 1053, D=64 868 / 897, D=32 662 / 629).
+// A 128-row tile with 64 keys runs as 64-row workgroups of four heads wherever the
+// 64-row tile would take four: each K/V tile is then staged for four heads instead of
+// two, and every 32-row wave computes the same either way (results bitwise equal).
+// Interleaved timings, two heads of 128 rows against four of 64: GQA B=2 H=32 H_kv=8
+// S=8192 D=128 +0.8 %, B=1 H=32 H_kv=4 S=8192 +0.9 %, B=2 H=32 H_kv=8 S=4096 +1.5 %,
+// MQA B=1 H=32 S=16384 D=64 fp16 +0.3 %, B=2 H=32 H_kv=8 S=8192 D=64 fp16 +0.7 %.
 int fwd_heads_per_wg(int B, int H, int group, int S, int D, int block_m, int block_n) {
+  auto four_fit = [&](int bm) {
+    return (long long)B * (H / 4) * ((S + bm - 1) / bm) >= (D <= 32 ? 4LL : 2LL) * cu_count();
+  };
+  if (block_m == 128 && block_n == 64 && heads_per_wg(group, 64, 64) == 4 && four_fit(64)) return 4;
   int gh = heads_per_wg(group, block_m, block_n);
-  const long long wgs = (long long)B * (H / 4) * ((S + block_m - 1) / block_m);
-  if (gh == 4 && wgs < (D <= 32 ? 4LL : 2LL) * cu_count()) gh = 2;
+  if (gh == 4 && !four_fit(block_m)) gh = 2;
   return gh;
 }
 
@@ -106,6 +115,7 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int D, int block_m, int blo
 // 973 -> 1003 with 64-key tiles and 681 -> 1019 with 128-key tiles, at D=32 739 -> 794
 // (the D = 32 backward +0.9-2.3 % at four shapes in A/B runs, -0.3 % at B=2 H=16 S=4096).
 int fwd_block_m(int block_m, int block_n, int D, int gh) {
+  if (gh == 4) return 64;  // four heads run 64-row tiles (fwd_heads_per_wg)
   return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
 }
 int dq_block_m(int block_m, int /*D*/) { return block_m == 64 ? 128 : block_m; }

@@ -228,7 +228,10 @@ def test_exact_shape_entries_and_rule_queries(lib):
     assert lib.fa_bwd_dq_rows_per_wg(64, 32) == 128 and lib.fa_bwd_dq_rows_per_wg(128, 32) == 128
     assert lib.fa_fwd_heads_per_wg(4, 32, 32, 4096, 128, 128, 64) == 1
     assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 64, 64) == 4
-    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 128, 64) == 2
+    assert lib.fa_fwd_heads_per_wg(2, 32, 8, 8192, 128, 128, 64) == 4   # 128-row tile as four 64-row heads
+    assert lib.fa_fwd_rows_per_wg(128, 64, 128, 4) == 64
+    assert lib.fa_fwd_heads_per_wg(1, 32, 1, 16384, 64, 128, 64) == 4
+    assert lib.fa_fwd_heads_per_wg(2, 8, 1, 2048, 128, 128, 64) == 2    # four would leave CUs short
     assert lib.fa_fwd_heads_per_wg(2, 8, 1, 1024, 128, 64, 64) == 2   # 4 -> 2: under 2 workgroups per CU
     assert lib.fa_fwd_heads_per_wg(1, 16, 4, 4096, 128, 64, 64) == 2  # one per CU at four heads
     assert lib.fa_fwd_heads_per_wg(2, 8, 1, 8192, 128, 64, 64) == 4   # two per CU: four stay
