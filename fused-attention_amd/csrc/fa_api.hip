@@ -110,13 +110,15 @@ int fwd_heads_per_wg(int B, int H, int group, int S, int D, int block_m, int blo
 // Forward, MHA B=4 H=32 S=4096 bf16, TFLOP/s of tile 64 -> 128 rows
 // (profiles/tile_study_mha_gqa_bwd.md): tile_n = 64: D=128 845 -> 1106 (MFMA busy
 // 43.9 -> 66.8 %: a 64-row workgroup holds one wave per SIMD), D=64 649 -> 922, D=32
-// 441 -> 675; tile_n = 128: D=128 464 -> 775 (D <= 64 about equal, so left).  dQ, every
+// 441 -> 675; tile_n = 128: D=128 464 -> 775, D=64 631 -> 654, D=32 447 -> 461 (the
+// D <= 64 forward at 128 keys +1.7-3.6 % at six shapes of A/B runs, -0.3 % at
+// B=4 H=32 D=32 bf16; four runs of the study read 128 rows 2-5 % faster).  dQ, every
 // head dim: 64 -> 128 rows at D=128 870 -> 1144 (MFMA busy 42.4 -> 62.2 %), at D=64
 // 973 -> 1003 with 64-key tiles and 681 -> 1019 with 128-key tiles, at D=32 739 -> 794
 // (the D = 32 backward +0.9-2.3 % at four shapes in A/B runs, -0.3 % at B=2 H=16 S=4096).
-int fwd_block_m(int block_m, int block_n, int D, int gh) {
+int fwd_block_m(int block_m, int /*block_n*/, int /*D*/, int gh) {
   if (gh == 4) return 64;  // four heads run 64-row tiles (fwd_heads_per_wg)
-  return (block_m == 64 && gh == 1 && (block_n == 64 || D == 128)) ? 128 : block_m;
+  return (block_m == 64 && gh == 1) ? 128 : block_m;
 }
 int dq_block_m(int block_m, int /*D*/) { return block_m == 64 ? 128 : block_m; }
 

@@ -223,7 +223,7 @@ def test_exact_shape_entries_and_rule_queries(lib):
 
     # the rules, as documented beside them in fa_api.hip
     assert lib.fa_fwd_rows_per_wg(64, 64, 128, 1) == 128 and lib.fa_fwd_rows_per_wg(64, 128, 128, 1) == 128
-    assert lib.fa_fwd_rows_per_wg(64, 128, 64, 1) == 64 and lib.fa_fwd_rows_per_wg(64, 64, 32, 2) == 64
+    assert lib.fa_fwd_rows_per_wg(64, 128, 64, 1) == 128 and lib.fa_fwd_rows_per_wg(64, 64, 32, 2) == 64
     assert lib.fa_bwd_dq_rows_per_wg(64, 128) == 128 and lib.fa_bwd_dq_rows_per_wg(64, 64) == 128
     assert lib.fa_bwd_dq_rows_per_wg(64, 32) == 128 and lib.fa_bwd_dq_rows_per_wg(128, 32) == 128
     assert lib.fa_fwd_heads_per_wg(4, 32, 32, 4096, 128, 128, 64) == 1
