@@ -1,11 +1,11 @@
 """fa_fwd_exact and fa_bwd_gqa_exact on the GPU, through the C ABI.
 
 These entry points (used by the tile study, no reference counterpart) run kernel instances
-the dispatch rules never reach: 64-row forward workgroups of one head at 64-key tiles, one,
-two or four GQA heads per workgroup where the rule picks another count, 64-row dQ
-workgroups at D >= 64, and any dK/dV split from 1 to 64 -- including more chunks than the
-heaviest key tile has (query tile, head) pairs, where some chunks are empty and store zero
-partial sums.
+the dispatch rules never reach: 64-row forward workgroups of one head, one, two or four GQA
+heads per workgroup where the rule picks another count (two heads of 128 rows where it takes
+four of 64), 64-row dQ workgroups, and any dK/dV split from 1 to 64 -- including more chunks
+than the heaviest key tile has (query tile, head) pairs, where some chunks are empty and store
+zero partial sums.
 
 Claims checked:
 * the workgroup shape does not change a result: a 32-row wave runs the same arithmetic over
@@ -95,7 +95,8 @@ def test_forward_exact_shapes_equal_dispatch_bitwise(B, H, Hkv, S, D, dtype):
     q, k, v, _ = inputs(B, H, Hkv, S, D, dtype, seed=S + D)
     o_ref, lse_ref = fwd(lib, q, k, v, 64, 64)
     g = H // Hkv
-    shapes = [(64, 64, gh) for gh in (1, 2, 4) if g % gh == 0] + [(128, 64, 1), (64, 128, 1)]
+    shapes = [(64, 64, gh) for gh in (1, 2, 4) if g % gh == 0] + [(128, 64, gh) for gh in (1, 2) if g % gh == 0]
+    shapes += [(64, 128, 1)]
     for bm, bn, gh in shapes:
         if bn == 128 and not lib.fa_supported(_lib.dtype_code(dtype), D, bm, bn, 1, 1, 0):
             continue
