@@ -112,6 +112,25 @@ def test_forward_exact_shapes_equal_dispatch_bitwise(B, H, Hkv, S, D, dtype):
         assert torch.equal(lse, lse_b), f"LSE of {bm}x{bn} with {gh} heads per workgroup"
 
 
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16)])
+def test_forward_gqa_tile_as_four_heads_bitwise(D, dtype):
+    """A 128-row, 64-key GQA tile runs as 64-row workgroups of four heads where the grid is large
+    enough (512 workgroups here, two per CU on a 256-CU device): the same O and LSE as two heads
+    of 128 rows and as four heads of 64."""
+    lib = _lib.load()
+    B, H, Hkv, S = 2, 8, 2, 8192
+    q, k, v, _ = inputs(B, H, Hkv, S, D, dtype, seed=D)
+    gh = lib.fa_fwd_heads_per_wg(B, H, Hkv, S, D, 128, 64)
+    rows = lib.fa_fwd_rows_per_wg(128, 64, D, gh)
+    o, lse = fwd(lib, q, k, v, 128, 64)
+    for bm, g in ((128, 2), (64, 4)):
+        o_x, lse_x = fwd(lib, q, k, v, bm, 64, g)
+        torch.cuda.synchronize()
+        log(f"fwd 128x64 dispatch ({gh} heads of {rows} rows) vs exact {g} heads of {bm} rows, D={D}: "
+            f"O maxdiff {float((o.float() - o_x.float()).abs().max()):.3g}")
+        assert torch.equal(o, o_x) and torch.equal(lse, lse_x), f"{g} heads of {bm} rows"
+
+
 BWD_CASES = [  # (B, H, H_kv, S, D, dtype): paired dK/dV at D = 128, one-wave at D = 64
     (1, 4, 2, 1000, 128, torch.bfloat16), (1, 4, 1, 700, 64, torch.float16),
 ]
